@@ -1,0 +1,122 @@
+/*
+ * packbalance_amd.h -- C ABI of the MI355X (gfx950) kernels behind PackBalance's
+ * training hot path: document-masked GQA attention, RMSNorm, SwiGLU and the
+ * LM-head cross-entropy.
+ *
+ * Conventions shared by every entry point
+ *   - Pointers are device pointers (HBM); sizes and strides are int64 element
+ *     counts; the innermost dimension of every matrix has unit stride.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the default stream).
+ *     Every entry point only enqueues work: no allocation, no host sync.
+ *   - Return value: PB_OK, or a negative status; pb_last_error() returns a
+ *     thread-local message describing the last failure on the calling thread.
+ *   - Inputs are never written.  Workspaces are caller-owned.
+ *
+ * Each declaration names the reference function it replaces
+ * (paths are relative to the DeKodez/packbalance source tree).
+ */
+#ifndef PACKBALANCE_AMD_H
+#define PACKBALANCE_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define PB_OK 0
+#define PB_EINVAL (-1)       /* bad shape / argument   -> Python ValueError   */
+#define PB_EUNSUPPORTED (-2) /* size/dtype not handled -> Python RuntimeError */
+#define PB_EHIP (-3)         /* HIP launch error       -> Python RuntimeError */
+
+/* ---- element types ------------------------------------------------------ */
+#define PB_F32 0
+#define PB_BF16 1
+#define PB_F16 2
+
+/* Message for the last failing call on this thread ("" if none). */
+const char *pb_last_error(void);
+
+/* ABI version of this library; bumped whenever a signature changes. */
+int pb_abi_version(void);
+
+/* ---- RMSNorm ------------------------------------------------------------
+ * Replaces packbalance/kernels/rmsnorm.py:29-48 (_rmsnorm_fwd) and the
+ * forward of _RMSNorm (rmsnorm.py:77-99).
+ *   rstd[r] = 1/sqrt(mean_c(x[r,c]^2) + eps)    (fp32)
+ *   y[r,c]  = x[r,c] * rstd[r] * w[c]            (fp32 math, stored as x_dtype)
+ * x_dtype, w_dtype in {PB_F32, PB_BF16, PB_F16}; y has x_dtype.
+ * n <= 65536 (rmsnorm.py:81-82 limit), else PB_EUNSUPPORTED.            */
+int pb_rmsnorm_fwd(const void *x, int64_t x_row_stride, int x_dtype,
+                   const void *w, int w_dtype, void *y, int64_t y_row_stride,
+                   float *rstd, int64_t rows, int64_t n, float eps,
+                   void *stream);
+
+/* Bytes of fp32 workspace pb_rmsnorm_bwd needs for its dw partial sums. */
+int64_t pb_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t n);
+
+/* Replaces rmsnorm.py:51-72 (_rmsnorm_bwd) and the eager dw reduction of
+ * _RMSNorm.backward (rmsnorm.py:117-118), fused:
+ *   g = dy*w, xh = x*rstd, dx = rstd*(g - xh*mean_c(g*xh))   (stored as dy dtype = x_dtype)
+ *   dw[c] = sum_r dy[r,c]*xh[r,c]   (fp32 accumulate, stored as w_dtype)
+ * `workspace` holds pb_rmsnorm_bwd_workspace_bytes(rows, n) bytes.          */
+int pb_rmsnorm_bwd(const void *dy, int64_t dy_row_stride, const void *x,
+                   int64_t x_row_stride, int x_dtype, const void *w,
+                   int w_dtype, const float *rstd, void *dx,
+                   int64_t dx_row_stride, void *dw, void *workspace,
+                   int64_t rows, int64_t n, void *stream);
+
+/* ---- SwiGLU -------------------------------------------------------------
+ * Replaces packbalance/kernels/swiglu.py:23-31 (_swiglu_fwd):
+ *   out = g*sigmoid(g)*u   over n contiguous elements (fp32 math).      */
+int pb_swiglu_fwd(const void *gate, const void *up, void *out, int64_t n,
+                  int dtype, void *stream);
+
+/* Replaces swiglu.py:34-46 (_swiglu_bwd):
+ *   dgate = dy*u*s*(1+g*(1-s)), dup = dy*g*s,  s = sigmoid(g).           */
+int pb_swiglu_bwd(const void *gate, const void *up, const void *dy,
+                  void *dgate, void *dup, int64_t n, int dtype, void *stream);
+
+/* ---- Row cross-entropy over a materialised logits block ----------------
+ * Replaces packbalance/kernels/fused_ce.py:31-89 (_ce_kernel) and
+ * _ce_launch (fused_ce.py:91-118).  Per row r of logits[m, v] (any strides):
+ *   lse = logsumexp_c logits[r,c]
+ *   loss[r] = lse - logits[r,t] + z*lse^2,    0 when t == ignore_index
+ *   dlogits[r,c] = softmax*(1+2z*lse) - [c==t], 0 rows for ignored targets
+ * dlogits (same dtype and strides as logits) is written only if non-NULL;
+ * lse_out (fp32 [m]) only if non-NULL.  targets are int64.  A target outside
+ * [0, v) that is not ignore_index is never dereferenced: its row's loss is
+ * NaN and its dlogits row carries no one-hot term.                          */
+int pb_ce_rows(const void *logits, int64_t stride_m, int64_t stride_v,
+               int dtype, const int64_t *targets, float *loss, float *lse_out,
+               void *dlogits, int64_t m, int64_t v, int64_t ignore_index,
+               float z_loss_coeff, void *stream);
+
+/* ---- Document block tables (FlexAttention BlockMask layout) -------------
+ * Replaces packbalance/model/attention.py:25-54 (build_doc_block_mask) with
+ * torch.nn.attention.flex_attention.create_block_mask's table semantics:
+ * mask(q, kv) = doc[q] == doc[kv] && q >= kv, positions >= s are masked,
+ * a block is FULL when all block*block entries are allowed, PARTIAL when
+ * some are.  Index rows list the set blocks ascending, then the unset blocks
+ * ascending (argsort(descending, stable)).
+ *   doc_ids  int64 [b, s] (row stride doc_stride)
+ *   outputs  int32, replicated over h heads, contiguous:
+ *     kv_num, full_kv_num        [b, h, nq]
+ *     kv_idx, full_kv_idx        [b, h, nq, nkv]
+ *     q_num, full_q_num          [b, h, nkv]
+ *     q_idx, full_q_idx          [b, h, nkv, nq]
+ *   with nq = nkv = ceil(s / block).
+ *   `class_ws` is a workspace of b*nq*nkv bytes (block class per tile).      */
+int pb_doc_block_tables(const int64_t *doc_ids, int64_t doc_stride, int64_t b,
+                        int64_t s, int64_t block, int64_t h, int32_t *kv_num,
+                        int32_t *kv_idx, int32_t *full_kv_num,
+                        int32_t *full_kv_idx, int32_t *q_num, int32_t *q_idx,
+                        int32_t *full_q_num, int32_t *full_q_idx,
+                        uint8_t *class_ws, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PACKBALANCE_AMD_H */

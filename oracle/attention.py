@@ -1,0 +1,127 @@
+"""CPU restatement of document-masked GQA attention (test oracle, float64).
+
+Reference: ``packbalance/model/attention.py``
+  * mask of the FlexAttention path:  doc[q] == doc[kv] and q >= kv   (:43-44)
+    -- padding tokens (doc_id = -1) form one more "document";
+  * ``eager_attention`` (:66-95): per document id >= 0, causal SDPA on that
+    document's tokens; rows with doc_id < 0 stay 0;
+  * GQA: query head h reads KV head h // (Hq/Hkv)  (repeat_interleave, :75-78;
+    ``enable_gqa`` in flex, :121); softmax scale 1/sqrt(D).
+
+``attention`` computes the forward (out, lse) and, given dO, the gradients
+with the standard closed forms
+    P = softmax(S), dV = P^T dO, dP = dO V^T, dS = P*(dP - rowsum(dO*O)),
+    dQ = scale*dS K, dK = scale*dS^T Q
+processed in query-row chunks so cfg-sized packs fit in host memory.  The
+closed forms are pinned against torch autograd in tests/test_oracle.py.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+
+def _chunk_rows(heads: int, keys: int, budget_bytes: int = 1 << 27) -> int:
+    per_row = max(1, heads * keys * 8)
+    return max(16, min(4096, budget_bytes // per_row))
+
+
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, doc_ids: torch.Tensor,
+              dout: torch.Tensor | None = None, *, semantics: str = "flex",
+              scale: float | None = None):
+    """Document-masked causal GQA attention in float64.
+
+    q [B, Hq, S, D], k/v [B, Hkv, S, D], doc_ids [B, S] (int), dout like q.
+    semantics: "flex"  -> mask_mod of attention.py:43-44 (pads attend to pads);
+               "eager" -> eager_attention of attention.py:66-95 (pad rows are 0
+                          and never attend or get attended).
+    Returns dict with out [B,Hq,S,D], lse [B,Hq,S] (natural log; -inf on rows
+    with no allowed key) and, if dout is given, dq, dk, dv (float64, CPU).
+    """
+    if semantics not in ("flex", "eager"):
+        raise ValueError(semantics)
+    B, Hq, S, D = q.shape
+    Hkv = k.shape[1]
+    if Hq % Hkv:
+        raise ValueError("Hq must be a multiple of Hkv")
+    G = Hq // Hkv
+    sc = 1.0 / math.sqrt(D) if scale is None else scale
+    dev = "cpu"
+    Q = q.detach().to(dev, torch.float64)
+    K = k.detach().to(dev, torch.float64).repeat_interleave(G, dim=1)
+    V = v.detach().to(dev, torch.float64).repeat_interleave(G, dim=1)
+    dO = None if dout is None else dout.detach().to(dev, torch.float64)
+    docs = doc_ids.detach().to(dev, torch.int64).reshape(B, S)
+
+    out = torch.zeros(B, Hq, S, D, dtype=torch.float64)
+    lse = torch.full((B, Hq, S), -math.inf, dtype=torch.float64)
+    dq = torch.zeros_like(out) if dO is not None else None
+    dk_full = torch.zeros(B, Hq, S, D, dtype=torch.float64) if dO is not None else None
+    dv_full = torch.zeros_like(dk_full) if dO is not None else None
+
+    pos = torch.arange(S)
+    for b in range(B):
+        doc = docs[b]
+        # For each query row, the first key it may see: the earliest key
+        # position with the same document id (general doc layouts allowed).
+        first = torch.empty(S, dtype=torch.int64)
+        seen: dict[int, int] = {}
+        for i, d in enumerate(doc.tolist()):
+            first[i] = seen.setdefault(d, i)
+        step = _chunk_rows(Hq, S)
+        for r0 in range(0, S, step):
+            r1 = min(S, r0 + step)
+            lo = int(first[r0:r1].min())
+            qi = pos[r0:r1]
+            ki = pos[lo:r1]
+            allowed = (doc[r0:r1, None] == doc[None, lo:r1]) & (qi[:, None] >= ki[None, :])
+            if semantics == "eager":
+                allowed &= (doc[r0:r1, None] >= 0) & (doc[None, lo:r1] >= 0)
+            s = torch.einsum("hqd,hkd->hqk", Q[b, :, r0:r1], K[b, :, lo:r1]) * sc
+            s = s.masked_fill(~allowed[None], -math.inf)
+            m = s.amax(dim=-1, keepdim=True)
+            has = torch.isfinite(m)
+            m = torch.where(has, m, torch.zeros_like(m))
+            p = torch.exp(s - m)
+            l = p.sum(dim=-1, keepdim=True)
+            p = torch.where(has, p / torch.where(has, l, torch.ones_like(l)), torch.zeros_like(p))
+            o = torch.einsum("hqk,hkd->hqd", p, V[b, :, lo:r1])
+            out[b, :, r0:r1] = o
+            lse[b, :, r0:r1] = torch.where(has[..., 0], (m + torch.log(l))[..., 0],
+                                           torch.full_like(m[..., 0], -math.inf))
+            if dO is not None:
+                do = dO[b, :, r0:r1]
+                dp = torch.einsum("hqd,hkd->hqk", do, V[b, :, lo:r1])
+                delta = (do * o).sum(dim=-1, keepdim=True)
+                ds = p * (dp - delta)
+                dq[b, :, r0:r1] = torch.einsum("hqk,hkd->hqd", ds, K[b, :, lo:r1]) * sc
+                dk_full[b, :, lo:r1] += torch.einsum("hqk,hqd->hkd", ds, Q[b, :, r0:r1]) * sc
+                dv_full[b, :, lo:r1] += torch.einsum("hqk,hqd->hkd", p, do)
+    res = {"out": out, "lse": lse}
+    if dO is not None:
+        res["dq"] = dq
+        res["dk"] = dk_full.reshape(B, Hkv, G, S, D).sum(dim=2)
+        res["dv"] = dv_full.reshape(B, Hkv, G, S, D).sum(dim=2)
+    return res
+
+
+def dense_mask(doc_ids: torch.Tensor) -> torch.Tensor:
+    """[B, S, S] bool mask of attention.py:43-44 (for the SDPA cross-check)."""
+    d = doc_ids.to(torch.int64)
+    S = d.shape[-1]
+    causal = torch.tril(torch.ones(S, S, dtype=torch.bool))
+    return (d[:, :, None] == d[:, None, :]) & causal
+
+
+def attention_flops(doc_lengths: list[int], head_dim: int, n_q_heads: int) -> dict[str, float]:
+    """Algorithmic FLOPs of masked attention: fwd 4*D*Hq*P, bwd 8*D*Hq*P.
+
+    P = sum over documents of L(L+1)/2 allowed (q, kv) pairs (causal within a
+    document) -- the counting of the reference's cost model
+    (``packbalance/data/cost.py:91-94,125-127``: train = 3 x forward).
+    """
+    pairs = float(sum(L * (L + 1) // 2 for L in doc_lengths))
+    return {"pairs": pairs, "fwd": 4.0 * head_dim * n_q_heads * pairs,
+            "bwd": 8.0 * head_dim * n_q_heads * pairs}

@@ -1,0 +1,129 @@
+"""CPU restatement of PackBalance's RMSNorm / SwiGLU / cross-entropy (test oracle).
+
+All math runs in float64 on the CPU unless a caller asks otherwise.  Inputs
+are taken as given (a bf16 tensor is first widened exactly to float64), so the
+oracle answers "what would exact arithmetic give on these stored values".
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+
+def _f64(t: torch.Tensor) -> torch.Tensor:
+    return t.detach().to("cpu", torch.float64)
+
+
+# ---------------------------------------------------------------- RMSNorm
+def rmsnorm_fwd(x: torch.Tensor, w: torch.Tensor, eps: float):
+    """y, rstd of reference ``kernels/reference.py:9-13`` and ``kernels/rmsnorm.py:40-47``.
+
+    rstd = 1/sqrt(mean(x^2) + eps) per row; y = x * rstd * w.
+    Returns (y [..., N] float64, rstd [rows] float64).
+    """
+    xf = _f64(x)
+    x2 = xf.reshape(-1, xf.shape[-1])
+    rstd = 1.0 / torch.sqrt((x2 * x2).mean(dim=-1) + eps)
+    y = x2 * rstd[:, None] * _f64(w)[None, :]
+    return y.reshape(xf.shape), rstd
+
+
+def rmsnorm_bwd(dy: torch.Tensor, x: torch.Tensor, w: torch.Tensor, eps: float):
+    """dx, dw of reference ``kernels/rmsnorm.py:63-71`` (dx) and ``:117-118`` (dw).
+
+    g = dy*w, x_hat = x*rstd, dx = rstd*(g - x_hat*mean(g*x_hat)),
+    dw = sum_rows dy*x_hat.  Pinned against autograd of rmsnorm_fwd.
+    """
+    xf = _f64(x)
+    n = xf.shape[-1]
+    x2 = xf.reshape(-1, n)
+    d2 = _f64(dy).reshape(-1, n)
+    _, rstd = rmsnorm_fwd(x, w, eps)
+    xh = x2 * rstd[:, None]
+    g = d2 * _f64(w)[None, :]
+    c = (g * xh).mean(dim=-1, keepdim=True)
+    dx = rstd[:, None] * (g - xh * c)
+    dw = (d2 * xh).sum(dim=0)
+    return dx.reshape(xf.shape), dw
+
+
+# ---------------------------------------------------------------- SwiGLU
+def swiglu_fwd(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """``silu(g)*u`` -- reference ``kernels/reference.py:16-17``, ``kernels/swiglu.py:28-30``."""
+    g, u = _f64(gate), _f64(up)
+    return g * torch.sigmoid(g) * u
+
+
+def swiglu_bwd(gate: torch.Tensor, up: torch.Tensor, dy: torch.Tensor):
+    """dgate, dup of reference ``kernels/swiglu.py:41-44``.
+
+    dg = dy*u*s*(1+g*(1-s)), du = dy*g*s with s = sigmoid(g).
+    Pinned against autograd of swiglu_fwd.
+    """
+    g, u, d = _f64(gate), _f64(up), _f64(dy)
+    s = torch.sigmoid(g)
+    return d * u * (s * (1.0 + g * (1.0 - s))), d * g * s
+
+
+# ---------------------------------------------------------------- cross-entropy
+def ce_rows(logits: torch.Tensor, targets: torch.Tensor, *, ignore_index: int = -100,
+            z_loss_coeff: float = 0.0, with_grad: bool = True):
+    """Per-row loss, lse and dlogits of reference ``kernels/fused_ce.py:45-89`` (_ce_kernel).
+
+    loss = lse - x_t + z*lse^2 (0 for ignored rows);
+    dlogits = softmax*(1+2z*lse) - onehot(t) (0 rows for ignored targets).
+    Returns (loss [M], lse [M], dlogits [M, V] or None), float64.
+    """
+    x = _f64(logits)
+    t = targets.detach().to("cpu", torch.int64).reshape(-1)
+    valid = t != ignore_index
+    safe_t = torch.where(valid, t, torch.zeros_like(t))
+    lse = torch.logsumexp(x, dim=-1)
+    tl = x.gather(1, safe_t[:, None])[:, 0]
+    loss = torch.where(valid, lse - tl + z_loss_coeff * lse * lse, torch.zeros_like(lse))
+    dl = None
+    if with_grad:
+        p = torch.softmax(x, dim=-1) * (1.0 + 2.0 * z_loss_coeff * lse)[:, None]
+        p[torch.arange(x.shape[0]), safe_t] -= 1.0
+        dl = torch.where(valid[:, None], p, torch.zeros_like(p))
+    return loss, lse, dl
+
+
+def linear_ce(x: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor, *,
+              ignore_index: int = -100, z_loss_coeff: float = 0.0, with_grad: bool = True):
+    """Summed CE of ``x @ W.T`` -- reference ``kernels/reference.py:20-48``.
+
+    Same contract as ``chunked_linear_cross_entropy`` / ``linear_cross_entropy``
+    (``kernels/fused_ce.py:205-217``): the SUM over rows with target !=
+    ignore_index of lse - logit_t + z*lse^2.  Row chunking does not change the
+    value, so the oracle uses one chunk.  Returns (loss, dx [x.shape], dW [V, D])
+    in float64; grads are those of the summed loss (grad_output = 1).
+    """
+    xf = _f64(x)
+    x2 = xf.reshape(-1, xf.shape[-1])
+    t = targets.detach().to("cpu", torch.int64).reshape(-1)
+    if x2.shape[0] != t.shape[0]:
+        raise ValueError(f"x has {x2.shape[0]} rows but targets has {t.shape[0]}")
+    w = _f64(weight)
+    logits = x2 @ w.t()
+    loss_rows, _, dl = ce_rows(logits, t, ignore_index=ignore_index,
+                               z_loss_coeff=z_loss_coeff, with_grad=with_grad)
+    loss = loss_rows.sum()
+    if not with_grad:
+        return loss, None, None
+    dx = (dl @ w).reshape(xf.shape)
+    dw = dl.t() @ x2
+    return loss, dx, dw
+
+
+def full_ce_reference(x: torch.Tensor, w: torch.Tensor, targets: torch.Tensor,
+                      z_loss_coeff: float = 0.0) -> torch.Tensor:
+    """The full-logits CE of reference ``tests/test_kernels.py:15-22`` (F.cross_entropy)."""
+    logits = x @ w.t()
+    loss = F.cross_entropy(logits, targets, ignore_index=-100, reduction="sum")
+    if z_loss_coeff:
+        lse = torch.logsumexp(logits.float(), dim=-1)
+        valid = targets != -100
+        loss = loss + z_loss_coeff * (lse[valid] ** 2).sum()
+    return loss

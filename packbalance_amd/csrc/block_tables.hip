@@ -1,0 +1,152 @@
+// Document block tables for packed sequences, for gfx950.
+//
+// Reference semantics: packbalance/model/attention.py:25-54 builds a
+// FlexAttention BlockMask from the mask
+//     allowed(q, kv) = doc[q] == doc[kv] && q >= kv
+// through torch's create_block_mask, which materialises the dense
+// [B, H, S, S] boolean mask, pads it with False to a multiple of the block
+// size, sums each block and classifies it EMPTY / PARTIAL / FULL, then orders
+// every row with argsort(descending, stable).
+//
+// Here the mask is never materialised.  Kernel 1 classifies every
+// (q-block, kv-block) tile straight from doc_ids staged in LDS (tiles with
+// kv-block > q-block are EMPTY by causality and exit at once).  Kernel 2
+// turns the class matrix into the eight int32 tables, one thread per
+// (batch, head, row), writing set indices ascending then unset indices
+// ascending -- the exact order of a stable descending argsort of a 0/1 row.
+#include "common.hpp"
+
+namespace pb {
+namespace {
+
+enum : uint8_t { kEmpty = 0, kPartial = 1, kFull = 2 };
+
+// grid = (nkv, nq, b); block = 256 threads.  qb x kb tile sizes in tokens.
+__global__ __launch_bounds__(256) void classify_tiles(const int64_t *__restrict__ doc,
+                                                      int64_t doc_stride, int64_t s, int qbs,
+                                                      int kbs, int nq, int nkv,
+                                                      uint8_t *__restrict__ cls) {
+  const int kb = blockIdx.x, qb = blockIdx.y, b = blockIdx.z;
+  uint8_t *out = cls + ((int64_t)b * nq + qb) * nkv + kb;
+  const int64_t q0 = (int64_t)qb * qbs, k0 = (int64_t)kb * kbs;
+  // Every kv in the tile lies after every q: masked by causality.
+  if (k0 > q0 + qbs - 1) {
+    if (threadIdx.x == 0) *out = kEmpty;
+    return;
+  }
+  extern __shared__ int64_t sdoc[];  // [qbs] q docs then [kbs] kv docs
+  int64_t *dq = sdoc, *dk = sdoc + qbs;
+  const int64_t *drow = doc + (int64_t)b * doc_stride;
+  for (int i = threadIdx.x; i < qbs; i += 256) dq[i] = (q0 + i < s) ? drow[q0 + i] : 0;
+  for (int i = threadIdx.x; i < kbs; i += 256) dk[i] = (k0 + i < s) ? drow[k0 + i] : 0;
+  __syncthreads();
+  int any = 0, all = 1;
+  const int pairs = qbs * kbs;
+  for (int p = threadIdx.x; p < pairs; p += 256) {
+    const int i = p / kbs, j = p - (p / kbs) * kbs;
+    const int64_t q = q0 + i, kv = k0 + j;
+    const bool ok = q < s && kv < s && q >= kv && dq[i] == dk[j];
+    any |= ok;
+    all &= ok;
+  }
+  any = __syncthreads_or(any);
+  all = __syncthreads_and(all);
+  if (threadIdx.x == 0) *out = all ? kFull : (any ? kPartial : kEmpty);
+}
+
+// One thread per (b, h, row) of either orientation.
+//   rows [0, nq)        -> kv tables (row = q-block, scan over kv-blocks)
+//   rows [nq, nq + nkv) -> q tables  (row = kv-block, scan over q-blocks)
+__global__ __launch_bounds__(256) void order_tables(const uint8_t *__restrict__ cls, int nb, int nh,
+                                                    int nq, int nkv, int32_t *kv_num,
+                                                    int32_t *kv_idx, int32_t *fkv_num,
+                                                    int32_t *fkv_idx, int32_t *q_num,
+                                                    int32_t *q_idx, int32_t *fq_num,
+                                                    int32_t *fq_idx) {
+  const int64_t tid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t per_bh = nq + nkv;
+  if (tid >= (int64_t)nb * nh * per_bh) return;
+  const int b = (int)(tid / ((int64_t)nh * per_bh));
+  const int64_t rem = tid - (int64_t)b * nh * per_bh;
+  const int h = (int)(rem / per_bh);
+  const int r = (int)(rem - (int64_t)h * per_bh);
+  const uint8_t *C = cls + (int64_t)b * nq * nkv;
+  const int64_t bh = (int64_t)b * nh + h;
+  if (r < nq) {
+    // kv-major tables for q-block r.
+    const int qb = r;
+    int32_t *pi = kv_idx + (bh * nq + qb) * nkv;
+    int32_t *fi = fkv_idx + (bh * nq + qb) * nkv;
+    int np = 0, nf = 0;
+    for (int k = 0; k < nkv; ++k) {
+      const uint8_t c = C[(int64_t)qb * nkv + k];
+      if (c == kPartial) pi[np++] = k;
+      if (c == kFull) fi[nf++] = k;
+    }
+    int tp = np, tf = nf;
+    for (int k = 0; k < nkv; ++k) {
+      const uint8_t c = C[(int64_t)qb * nkv + k];
+      if (c != kPartial) pi[tp++] = k;
+      if (c != kFull) fi[tf++] = k;
+    }
+    kv_num[bh * nq + qb] = np;
+    fkv_num[bh * nq + qb] = nf;
+  } else {
+    const int kb = r - nq;
+    int32_t *pi = q_idx + (bh * nkv + kb) * nq;
+    int32_t *fi = fq_idx + (bh * nkv + kb) * nq;
+    int np = 0, nf = 0;
+    for (int q = 0; q < nq; ++q) {
+      const uint8_t c = C[(int64_t)q * nkv + kb];
+      if (c == kPartial) pi[np++] = q;
+      if (c == kFull) fi[nf++] = q;
+    }
+    int tp = np, tf = nf;
+    for (int q = 0; q < nq; ++q) {
+      const uint8_t c = C[(int64_t)q * nkv + kb];
+      if (c != kPartial) pi[tp++] = q;
+      if (c != kFull) fi[tf++] = q;
+    }
+    q_num[bh * nkv + kb] = np;
+    fq_num[bh * nkv + kb] = nf;
+  }
+}
+
+}  // namespace
+
+// Shared with the attention planner: classify tiles of qbs x kbs tokens.
+int classify_doc_tiles(const int64_t *doc, int64_t doc_stride, int64_t b, int64_t s, int qbs,
+                       int kbs, uint8_t *cls, hipStream_t st) {
+  const int nq = (int)((s + qbs - 1) / qbs), nkv = (int)((s + kbs - 1) / kbs);
+  dim3 grid(nkv, nq, (unsigned)b);
+  const size_t lds = (size_t)(qbs + kbs) * sizeof(int64_t);
+  hipLaunchKernelGGL(classify_tiles, grid, dim3(256), lds, st, doc, doc_stride, s, qbs, kbs, nq, nkv,
+                     cls);
+  return launch_status("classify_doc_tiles");
+}
+
+}  // namespace pb
+
+extern "C" int pb_doc_block_tables(const int64_t *doc_ids, int64_t doc_stride, int64_t b,
+                                   int64_t s, int64_t block, int64_t h, int32_t *kv_num,
+                                   int32_t *kv_idx, int32_t *full_kv_num, int32_t *full_kv_idx,
+                                   int32_t *q_num, int32_t *q_idx, int32_t *full_q_num,
+                                   int32_t *full_q_idx, uint8_t *class_ws, void *stream) {
+  using namespace pb;
+  clear_error();
+  PB_CHECK_ARG(b >= 1 && s >= 1 && h >= 1, "pb_doc_block_tables: bad shape b=%lld s=%lld h=%lld",
+               (long long)b, (long long)s, (long long)h);
+  PB_CHECK_ARG(block >= 1 && block <= 1024, "pb_doc_block_tables: block size %lld out of [1, 1024]",
+               (long long)block);
+  PB_CHECK_ARG(doc_stride >= s, "pb_doc_block_tables: doc_stride < s");
+  const int64_t nblk = (s + block - 1) / block;
+  PB_CHECK_SUPPORTED(nblk <= 65535 && b <= 65535, "pb_doc_block_tables: too many blocks");
+  hipStream_t st = as_stream(stream);
+  int rc = classify_doc_tiles(doc_ids, doc_stride, b, s, (int)block, (int)block, class_ws, st);
+  if (rc) return rc;
+  const int64_t threads = b * h * (2 * nblk);
+  hipLaunchKernelGGL(order_tables, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
+                     class_ws, (int)b, (int)h, (int)nblk, (int)nblk, kv_num, kv_idx, full_kv_num,
+                     full_kv_idx, q_num, q_idx, full_q_num, full_q_idx);
+  return launch_status("pb_doc_block_tables");
+}

@@ -1,0 +1,129 @@
+// Shared device/host helpers for the gfx950 kernels: status reporting,
+// element-type conversion, 128-bit vector access and wave64 reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdarg>
+#include <cstdio>
+
+#include "../../include/packbalance_amd.h"
+
+namespace pb {
+
+// ---------------------------------------------------------------- status
+// One message per host thread: forward runs on the Python thread, backward
+// on autograd's device thread, so the message must not be shared.
+void set_error(const char *fmt, ...);
+void clear_error();
+
+#define PB_CHECK_ARG(cond, ...)            \
+  do {                                     \
+    if (!(cond)) {                         \
+      ::pb::set_error(__VA_ARGS__);        \
+      return PB_EINVAL;                    \
+    }                                      \
+  } while (0)
+
+#define PB_CHECK_SUPPORTED(cond, ...)      \
+  do {                                     \
+    if (!(cond)) {                         \
+      ::pb::set_error(__VA_ARGS__);        \
+      return PB_EUNSUPPORTED;              \
+    }                                      \
+  } while (0)
+
+// Launch status of the most recent kernel on this thread.
+int launch_status(const char *what);
+
+inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline bool valid_dtype(int dt) { return dt == PB_F32 || dt == PB_BF16 || dt == PB_F16; }
+inline int dtype_bytes(int dt) { return dt == PB_F32 ? 4 : 2; }
+
+// ---------------------------------------------------------------- types
+typedef __bf16 bf16_t;
+typedef _Float16 f16_t;
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T> __device__ __forceinline__ float to_f32(T v) { return static_cast<float>(v); }
+template <typename T> __device__ __forceinline__ T from_f32(float v) { return static_cast<T>(v); }
+
+// A 16-byte vector of T: the unit of every coalesced global access.
+template <typename T> struct Vec16 {
+  static constexpr int N = 16 / sizeof(T);
+  T v[N];
+};
+
+template <typename T>
+__device__ __forceinline__ void load16(const T *p, float (&out)[16 / sizeof(T)]) {
+  constexpr int N = 16 / sizeof(T);
+  u32x4 raw = *reinterpret_cast<const u32x4 *>(p);
+  const T *e = reinterpret_cast<const T *>(&raw);
+#pragma unroll
+  for (int i = 0; i < N; ++i) out[i] = to_f32(e[i]);
+}
+
+template <typename T>
+__device__ __forceinline__ void store16(T *p, const float (&in)[16 / sizeof(T)]) {
+  constexpr int N = 16 / sizeof(T);
+  u32x4 raw;
+  T *e = reinterpret_cast<T *>(&raw);
+#pragma unroll
+  for (int i = 0; i < N; ++i) e[i] = from_f32<T>(in[i]);
+  *reinterpret_cast<u32x4 *>(p) = raw;
+}
+
+// Non-temporal variants for streams that are touched exactly once.
+template <typename T>
+__device__ __forceinline__ void load16_nt(const T *p, float (&out)[16 / sizeof(T)]) {
+  constexpr int N = 16 / sizeof(T);
+  u32x4 raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+  const T *e = reinterpret_cast<const T *>(&raw);
+#pragma unroll
+  for (int i = 0; i < N; ++i) out[i] = to_f32(e[i]);
+}
+
+template <typename T>
+__device__ __forceinline__ void store16_nt(T *p, const float (&in)[16 / sizeof(T)]) {
+  constexpr int N = 16 / sizeof(T);
+  u32x4 raw;
+  T *e = reinterpret_cast<T *>(&raw);
+#pragma unroll
+  for (int i = 0; i < N; ++i) e[i] = from_f32<T>(in[i]);
+  __builtin_nontemporal_store(raw, reinterpret_cast<u32x4 *>(p));
+}
+
+// ---------------------------------------------------------------- wave64
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+// Fast transcendental helpers on the hardware exp2/log2/rcp units.
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float sigmoid(float g) {
+  // 1 / (1 + 2^(-g*log2 e)); exp2 of a large argument gives +inf and rcp(inf)=0.
+  return fast_rcp(1.0f + fast_exp2(-g * kLog2e));
+}
+
+}  // namespace pb

@@ -1,0 +1,418 @@
+// RMSNorm forward and backward for gfx950.
+//
+// Reference semantics: packbalance/kernels/rmsnorm.py:29-72 (Triton kernels)
+// and rmsnorm.py:77-119 (_RMSNorm: rstd cached in fp32, dw = sum_r dy*x_hat).
+//
+// Layout: one 64-lane wavefront owns one row at a time; every lane moves
+// 16-byte vectors, so a row of n elements is read as n*sizeof(T)/1024
+// fully-coalesced wave loads.  When a row fits in registers (n <= 64*VEC*NV)
+// it is read from HBM exactly once; the reduction is a wave64 butterfly, so
+// no LDS or block barrier sits on the forward path.  The backward also
+// accumulates the per-column dw partial sums of the rows a workgroup owns and
+// writes one fp32 partial row per workgroup; a second small kernel sums the
+// partials (the reference does this with two extra eager passes over x, dy).
+#include "common.hpp"
+
+namespace pb {
+namespace {
+
+constexpr int kWaves = 4;  // waves per workgroup
+constexpr int kThreads = 64 * kWaves;
+
+// Load `N` consecutive elements of T at p (p aligned to N*sizeof(T) bytes up
+// to 16) into fp32.
+template <typename T, int N>
+__device__ __forceinline__ void load_vec(const T *p, float (&o)[N]) {
+  constexpr int kBytes = N * sizeof(T);
+  static_assert(kBytes % 8 == 0, "vector of at least 8 bytes");
+  if constexpr (kBytes >= 16) {
+#pragma unroll
+    for (int c = 0; c < kBytes / 16; ++c) {
+      u32x4 raw = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const char *>(p) + 16 * c);
+      const T *e = reinterpret_cast<const T *>(&raw);
+#pragma unroll
+      for (int i = 0; i < 16 / (int)sizeof(T); ++i) o[c * (16 / sizeof(T)) + i] = to_f32(e[i]);
+    }
+  } else {
+    u32x2 raw = *reinterpret_cast<const u32x2 *>(p);
+    const T *e = reinterpret_cast<const T *>(&raw);
+#pragma unroll
+    for (int i = 0; i < N; ++i) o[i] = to_f32(e[i]);
+  }
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void store_vec(T *p, const float (&v)[N]) {
+  static_assert(N * sizeof(T) == 16, "16-byte store");
+  u32x4 raw;
+  T *e = reinterpret_cast<T *>(&raw);
+#pragma unroll
+  for (int i = 0; i < N; ++i) e[i] = from_f32<T>(v[i]);
+  *reinterpret_cast<u32x4 *>(p) = raw;
+}
+
+// ---------------------------------------------------------------- forward
+// Register-resident row: NV vectors of VEC elements per lane.
+template <typename TX, typename TW, int NV>
+__global__ __launch_bounds__(kThreads) void rmsnorm_fwd_reg(
+    const TX *__restrict__ x, int64_t xs, const TW *__restrict__ w, TX *__restrict__ y, int64_t ys,
+    float *__restrict__ rstd_out, int64_t rows, int n, float eps) {
+  constexpr int VEC = 16 / sizeof(TX);
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const TX *xr = x + row * xs;
+  float v[NV][VEC];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = (i * 64 + lane) * VEC;
+    if (c < n) {
+      load_vec<TX, VEC>(xr + c, v[i]);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) ss += v[i][e] * v[i][e];
+    }
+  }
+  ss = wave_sum(ss);
+  const float r = 1.0f / sqrtf(ss / (float)n + eps);
+  if (lane == 0) rstd_out[row] = r;
+  TX *yr = y + row * ys;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = (i * 64 + lane) * VEC;
+    if (c < n) {
+      float wv[VEC];
+      load_vec<TW, VEC>(w + c, wv);
+      float o[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) o[e] = v[i][e] * r * wv[e];
+      store_vec<TX, VEC>(yr + c, o);
+    }
+  }
+}
+
+// General row (any n, any alignment): two passes over the row, scalar loads.
+template <typename TX, typename TW>
+__global__ __launch_bounds__(kThreads) void rmsnorm_fwd_loop(
+    const TX *__restrict__ x, int64_t xs, const TW *__restrict__ w, TX *__restrict__ y, int64_t ys,
+    float *__restrict__ rstd_out, int64_t rows, int n, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const TX *xr = x + row * xs;
+  float ss = 0.f;
+  for (int c = lane; c < n; c += 64) {
+    float t = to_f32(xr[c]);
+    ss += t * t;
+  }
+  ss = wave_sum(ss);
+  const float r = 1.0f / sqrtf(ss / (float)n + eps);
+  if (lane == 0) rstd_out[row] = r;
+  TX *yr = y + row * ys;
+  for (int c = lane; c < n; c += 64) yr[c] = from_f32<TX>(to_f32(xr[c]) * r * to_f32(w[c]));
+}
+
+// ---------------------------------------------------------------- backward
+// Each workgroup owns rows [blockIdx.x*rows_per_wg, ...), its waves take
+// every kWaves-th row; dw partials are reduced across the waves in LDS and
+// written as one fp32 row per workgroup.
+template <typename TX, typename TW, int NV>
+__global__ __launch_bounds__(kThreads) void rmsnorm_bwd_reg(
+    const TX *__restrict__ dy, int64_t dys, const TX *__restrict__ x, int64_t xs,
+    const TW *__restrict__ w, const float *__restrict__ rstd, TX *__restrict__ dx, int64_t dxs,
+    float *__restrict__ partial, int64_t rows, int n, int rows_per_wg) {
+  constexpr int VEC = 16 / sizeof(TX);
+  __shared__ float red[kWaves - 1][NV * VEC * 64];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const float inv_n = 1.0f / (float)n;
+  float acc[NV][VEC];
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[i][e] = 0.f;
+
+  const int64_t r0 = (int64_t)blockIdx.x * rows_per_wg;
+  const int64_t r1 = r0 + rows_per_wg < rows ? r0 + rows_per_wg : rows;
+  for (int64_t row = r0 + wave; row < r1; row += kWaves) {
+    const float r = rstd[row];
+    float xh[NV][VEC], g[NV][VEC];
+    float dot = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = (i * 64 + lane) * VEC;
+      if (c < n) {
+        float dv[VEC], wv[VEC];
+        load_vec<TX, VEC>(x + row * xs + c, xh[i]);
+        load_vec<TX, VEC>(dy + row * dys + c, dv);
+        load_vec<TW, VEC>(w + c, wv);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          xh[i][e] *= r;
+          g[i][e] = dv[e] * wv[e];
+          dot += g[i][e] * xh[i][e];
+          acc[i][e] += dv[e] * xh[i][e];
+        }
+      }
+    }
+    dot = wave_sum(dot) * inv_n;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = (i * 64 + lane) * VEC;
+      if (c < n) {
+        float o[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o[e] = r * (g[i][e] - xh[i][e] * dot);
+        store_vec<TX, VEC>(dx + row * dxs + c, o);
+      }
+    }
+  }
+  // Cross-wave reduction of the dw partial (columns are lane-private).
+  if (wave > 0) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) red[wave - 1][(i * VEC + e) * 64 + lane] = acc[i][e];
+  }
+  __syncthreads();
+  if (wave == 0) {
+    float *out = partial + (int64_t)blockIdx.x * n;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = (i * 64 + lane) * VEC;
+      if (c < n) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          float s = acc[i][e];
+#pragma unroll
+          for (int k = 0; k < kWaves - 1; ++k) s += red[k][(i * VEC + e) * 64 + lane];
+          out[c + e] = s;
+        }
+      }
+    }
+  }
+}
+
+template <typename TX, typename TW>
+__global__ __launch_bounds__(kThreads) void rmsnorm_bwd_loop(
+    const TX *__restrict__ dy, int64_t dys, const TX *__restrict__ x, int64_t xs,
+    const TW *__restrict__ w, const float *__restrict__ rstd, TX *__restrict__ dx, int64_t dxs,
+    float *__restrict__ partial, int64_t rows, int n, int rows_per_wg) {
+  // Columns strided over all 256 threads; rows walked sequentially by the
+  // whole workgroup, with the row dot product reduced through LDS.
+  __shared__ float red[kWaves];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const float inv_n = 1.0f / (float)n;
+  const int64_t r0 = (int64_t)blockIdx.x * rows_per_wg;
+  const int64_t r1 = r0 + rows_per_wg < rows ? r0 + rows_per_wg : rows;
+  float *out = partial + (int64_t)blockIdx.x * n;
+  for (int c = threadIdx.x; c < n; c += kThreads) out[c] = 0.f;
+  __syncthreads();
+  for (int64_t row = r0; row < r1; ++row) {
+    const float r = rstd[row];
+    float dot = 0.f;
+    for (int c = threadIdx.x; c < n; c += kThreads)
+      dot += to_f32(dy[row * dys + c]) * to_f32(w[c]) * to_f32(x[row * xs + c]) * r;
+    dot = wave_sum(dot);
+    if (lane == 0) red[wave] = dot;
+    __syncthreads();
+    dot = 0.f;
+#pragma unroll
+    for (int k = 0; k < kWaves; ++k) dot += red[k];
+    dot *= inv_n;
+    __syncthreads();
+    for (int c = threadIdx.x; c < n; c += kThreads) {
+      const float xh = to_f32(x[row * xs + c]) * r;
+      const float d = to_f32(dy[row * dys + c]);
+      const float g = d * to_f32(w[c]);
+      dx[row * dxs + c] = from_f32<TX>(r * (g - xh * dot));
+      out[c] += d * xh;  // column c is private to this thread
+    }
+  }
+}
+
+// dw[c] = sum_p partial[p, c]; 64 columns x 4 partial-row groups per block.
+template <typename TW>
+__global__ __launch_bounds__(256) void rmsnorm_dw_reduce(const float *__restrict__ partial,
+                                                         TW *__restrict__ dw, int nparts, int n) {
+  __shared__ float red[4][64];
+  const int col = blockIdx.x * 64 + (threadIdx.x & 63);
+  const int grp = threadIdx.x >> 6;
+  float s = 0.f;
+  if (col < n)
+    for (int p = grp; p < nparts; p += 4) s += partial[(int64_t)p * n + col];
+  red[grp][threadIdx.x & 63] = s;
+  __syncthreads();
+  if (grp == 0 && col < n) dw[col] = from_f32<TW>(red[0][threadIdx.x] + red[1][threadIdx.x] +
+                                                  red[2][threadIdx.x] + red[3][threadIdx.x]);
+}
+
+// ---------------------------------------------------------------- dispatch
+struct BwdPlan {
+  int rows_per_wg;
+  int nwg;
+};
+
+BwdPlan bwd_plan(int64_t rows) {
+  // Aim for ~1024 workgroups (4 per CU) so the partial rows stay a small
+  // fraction of the traffic; never fewer than kWaves rows per workgroup.
+  int64_t rpw = (rows + 1023) / 1024;
+  if (rpw < kWaves) rpw = kWaves;
+  BwdPlan p;
+  p.rows_per_wg = (int)rpw;
+  p.nwg = (int)((rows + rpw - 1) / rpw);
+  if (p.nwg < 1) p.nwg = 1;
+  return p;
+}
+
+// Number of 16-byte vectors per lane that a register-resident row needs,
+// rounded up to the instantiated set; 0 when the row must stream.
+template <typename TX>
+int pick_nv(int64_t n, const void *a, int64_t a_stride, const void *b, int64_t b_stride,
+            const void *c, int64_t c_stride) {
+  constexpr int VEC = 16 / sizeof(TX);
+  if (n % VEC) return 0;
+  auto aligned = [](const void *p, int64_t stride) {
+    return p == nullptr ||
+           ((reinterpret_cast<uintptr_t>(p) % 16 == 0) && ((stride * (int64_t)sizeof(TX)) % 16 == 0));
+  };
+  if (!aligned(a, a_stride) || !aligned(b, b_stride) || !aligned(c, c_stride)) return 0;
+  const int64_t need = (n + 64 * VEC - 1) / (64 * VEC);
+  if (need <= 1) return 1;
+  if (need <= 2) return 2;
+  if (need <= 4) return 4;
+  if (need <= 8) return 8;
+  return 0;
+}
+
+template <typename TX, typename TW>
+int fwd_typed(const void *x, int64_t xs, const void *w, void *y, int64_t ys, float *rstd,
+              int64_t rows, int64_t n, float eps, hipStream_t st) {
+  const TX *X = static_cast<const TX *>(x);
+  const TW *W = static_cast<const TW *>(w);
+  TX *Y = static_cast<TX *>(y);
+  dim3 grid((unsigned)((rows + kWaves - 1) / kWaves));
+  int nv = pick_nv<TX>(n, x, xs, y, ys, nullptr, 0);
+  if (nv && (reinterpret_cast<uintptr_t>(w) % (16 / sizeof(TX) * sizeof(TW) >= 16 ? 16 : 8)) != 0)
+    nv = 0;
+  switch (nv) {
+#define PB_FWD(NV)                                                                               \
+  case NV:                                                                                       \
+    hipLaunchKernelGGL((rmsnorm_fwd_reg<TX, TW, NV>), grid, dim3(kThreads), 0, st, X, xs, W, Y,  \
+                       ys, rstd, rows, (int)n, eps);                                             \
+    break;
+    PB_FWD(1) PB_FWD(2) PB_FWD(4) PB_FWD(8)
+#undef PB_FWD
+    default:
+      hipLaunchKernelGGL((rmsnorm_fwd_loop<TX, TW>), grid, dim3(kThreads), 0, st, X, xs, W, Y, ys,
+                         rstd, rows, (int)n, eps);
+  }
+  return launch_status("pb_rmsnorm_fwd");
+}
+
+template <typename TX, typename TW>
+int bwd_typed(const void *dy, int64_t dys, const void *x, int64_t xs, const void *w,
+              const float *rstd, void *dx, int64_t dxs, void *dw, float *ws, int64_t rows,
+              int64_t n, hipStream_t st) {
+  const TX *DY = static_cast<const TX *>(dy);
+  const TX *X = static_cast<const TX *>(x);
+  const TW *W = static_cast<const TW *>(w);
+  TX *DX = static_cast<TX *>(dx);
+  BwdPlan p = bwd_plan(rows);
+  int nv = pick_nv<TX>(n, x, xs, dy, dys, dx, dxs);
+  if (nv && (reinterpret_cast<uintptr_t>(w) % (16 / sizeof(TX) * sizeof(TW) >= 16 ? 16 : 8)) != 0)
+    nv = 0;
+  dim3 grid(p.nwg);
+  switch (nv) {
+#define PB_BWD(NV)                                                                              \
+  case NV:                                                                                      \
+    hipLaunchKernelGGL((rmsnorm_bwd_reg<TX, TW, NV>), grid, dim3(kThreads), 0, st, DY, dys, X,  \
+                       xs, W, rstd, DX, dxs, ws, rows, (int)n, p.rows_per_wg);                  \
+    break;
+    PB_BWD(1) PB_BWD(2) PB_BWD(4) PB_BWD(8)
+#undef PB_BWD
+    default:
+      hipLaunchKernelGGL((rmsnorm_bwd_loop<TX, TW>), grid, dim3(kThreads), 0, st, DY, dys, X, xs,
+                         W, rstd, DX, dxs, ws, rows, (int)n, p.rows_per_wg);
+  }
+  int s = launch_status("pb_rmsnorm_bwd");
+  if (s) return s;
+  hipLaunchKernelGGL((rmsnorm_dw_reduce<TW>), dim3((unsigned)((n + 63) / 64)), dim3(256), 0, st,
+                     ws, static_cast<TW *>(dw), p.nwg, (int)n);
+  return launch_status("pb_rmsnorm_bwd(dw)");
+}
+
+template <typename TX>
+int fwd_w(int wdt, const void *x, int64_t xs, const void *w, void *y, int64_t ys, float *rstd,
+          int64_t rows, int64_t n, float eps, hipStream_t st) {
+  switch (wdt) {
+    case PB_F32: return fwd_typed<TX, float>(x, xs, w, y, ys, rstd, rows, n, eps, st);
+    case PB_BF16: return fwd_typed<TX, bf16_t>(x, xs, w, y, ys, rstd, rows, n, eps, st);
+    default: return fwd_typed<TX, f16_t>(x, xs, w, y, ys, rstd, rows, n, eps, st);
+  }
+}
+
+template <typename TX>
+int bwd_w(int wdt, const void *dy, int64_t dys, const void *x, int64_t xs, const void *w,
+          const float *rstd, void *dx, int64_t dxs, void *dw, float *ws, int64_t rows, int64_t n,
+          hipStream_t st) {
+  switch (wdt) {
+    case PB_F32: return bwd_typed<TX, float>(dy, dys, x, xs, w, rstd, dx, dxs, dw, ws, rows, n, st);
+    case PB_BF16: return bwd_typed<TX, bf16_t>(dy, dys, x, xs, w, rstd, dx, dxs, dw, ws, rows, n, st);
+    default: return bwd_typed<TX, f16_t>(dy, dys, x, xs, w, rstd, dx, dxs, dw, ws, rows, n, st);
+  }
+}
+
+}  // namespace
+}  // namespace pb
+
+extern "C" int pb_rmsnorm_fwd(const void *x, int64_t x_row_stride, int x_dtype, const void *w,
+                              int w_dtype, void *y, int64_t y_row_stride, float *rstd,
+                              int64_t rows, int64_t n, float eps, void *stream) {
+  using namespace pb;
+  clear_error();
+  PB_CHECK_ARG(valid_dtype(x_dtype) && valid_dtype(w_dtype), "pb_rmsnorm_fwd: bad dtype");
+  PB_CHECK_ARG(rows >= 0 && n > 0, "pb_rmsnorm_fwd: bad shape rows=%lld n=%lld", (long long)rows,
+               (long long)n);
+  PB_CHECK_SUPPORTED(n <= 65536, "RMSNorm feature dimension is too large for this kernel");
+  PB_CHECK_ARG(x_row_stride >= n && y_row_stride >= n, "pb_rmsnorm_fwd: row stride < n");
+  if (rows == 0) return PB_OK;
+  hipStream_t st = as_stream(stream);
+  switch (x_dtype) {
+    case PB_F32: return fwd_w<float>(w_dtype, x, x_row_stride, w, y, y_row_stride, rstd, rows, n, eps, st);
+    case PB_BF16: return fwd_w<bf16_t>(w_dtype, x, x_row_stride, w, y, y_row_stride, rstd, rows, n, eps, st);
+    default: return fwd_w<f16_t>(w_dtype, x, x_row_stride, w, y, y_row_stride, rstd, rows, n, eps, st);
+  }
+}
+
+extern "C" int64_t pb_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t n) {
+  if (rows <= 0 || n <= 0) return 0;
+  return (int64_t)pb::bwd_plan(rows).nwg * n * (int64_t)sizeof(float);
+}
+
+extern "C" int pb_rmsnorm_bwd(const void *dy, int64_t dy_row_stride, const void *x,
+                              int64_t x_row_stride, int x_dtype, const void *w, int w_dtype,
+                              const float *rstd, void *dx, int64_t dx_row_stride, void *dw,
+                              void *workspace, int64_t rows, int64_t n, void *stream) {
+  using namespace pb;
+  clear_error();
+  PB_CHECK_ARG(valid_dtype(x_dtype) && valid_dtype(w_dtype), "pb_rmsnorm_bwd: bad dtype");
+  PB_CHECK_ARG(rows >= 0 && n > 0, "pb_rmsnorm_bwd: bad shape");
+  PB_CHECK_SUPPORTED(n <= 65536, "RMSNorm feature dimension is too large for this kernel");
+  PB_CHECK_ARG(x_row_stride >= n && dy_row_stride >= n && dx_row_stride >= n,
+               "pb_rmsnorm_bwd: row stride < n");
+  hipStream_t st = as_stream(stream);
+  if (rows == 0) {
+    // dw of an empty batch is zero.
+    hipMemsetAsync(dw, 0, (size_t)n * dtype_bytes(w_dtype), st);
+    return launch_status("pb_rmsnorm_bwd(empty)");
+  }
+  PB_CHECK_ARG(workspace != nullptr, "pb_rmsnorm_bwd: workspace is required");
+  float *ws = static_cast<float *>(workspace);
+  switch (x_dtype) {
+    case PB_F32: return bwd_w<float>(w_dtype, dy, dy_row_stride, x, x_row_stride, w, rstd, dx, dx_row_stride, dw, ws, rows, n, st);
+    case PB_BF16: return bwd_w<bf16_t>(w_dtype, dy, dy_row_stride, x, x_row_stride, w, rstd, dx, dx_row_stride, dw, ws, rows, n, st);
+    default: return bwd_w<f16_t>(w_dtype, dy, dy_row_stride, x, x_row_stride, w, rstd, dx, dx_row_stride, dw, ws, rows, n, st);
+  }
+}

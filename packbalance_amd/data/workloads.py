@@ -1,0 +1,155 @@
+"""Synthetic packed workloads of the benchmark configurations.
+
+Document lengths are drawn like the reference's synthetic corpus
+(``packbalance/data/prepare.py:59-65``: lognormal, truncated to int, clipped),
+packed best-fit-decreasing like ``packbalance/data/packer.py:87-144``
+(segments sorted by (-length, doc_id); each goes to the bin with the smallest
+remaining capacity that fits, found by bisection), and turned into model
+tensors with the conventions of ``packbalance/data/dataset.py:33-76``:
+``doc_ids`` are 0..n-1 per pack and -1 on padding, ``position_ids`` restart at
+0 in every document, ``labels`` are the next token inside a document and -100
+on each document's last token and on padding.
+"""
+
+from __future__ import annotations
+
+import bisect
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+
+def lognormal_lengths(rng: np.random.Generator, n: int, mu: float, sigma: float, lo: int,
+                      hi: int) -> np.ndarray:
+    lengths = rng.lognormal(mean=mu, sigma=sigma, size=n).astype(np.int64)
+    return np.clip(lengths, lo, hi)
+
+
+def best_fit_decreasing(lengths: np.ndarray, seq_len: int) -> list[list[int]]:
+    """Bins of document lengths (each bin lists its documents' lengths in placement order)."""
+    order = sorted(range(len(lengths)), key=lambda i: (-int(lengths[i]), i))
+    bins: list[list[int]] = []
+    keys: list[int] = []  # remaining capacities, ascending
+    ids: list[int] = []
+    for i in order:
+        n = int(lengths[i])
+        if n > seq_len:
+            raise ValueError(f"document of {n} tokens does not fit seq_len {seq_len}")
+        pos = bisect.bisect_left(keys, n)
+        if pos == len(keys):
+            bid = len(bins)
+            bins.append([n])
+            rem = seq_len - n
+        else:
+            bid = ids.pop(pos)
+            rem = keys.pop(pos) - n
+            bins[bid].append(n)
+        p = bisect.bisect_left(keys, rem)
+        keys.insert(p, rem)
+        ids.insert(p, bid)
+    return bins
+
+
+def fill_sequential(rng: np.random.Generator, seq_len: int, mu: float, sigma: float, lo: int,
+                    hi: int) -> list[int]:
+    """Documents drawn one after another, the last one truncated to fill seq_len exactly."""
+    out: list[int] = []
+    used = 0
+    while used < seq_len:
+        n = int(lognormal_lengths(rng, 1, mu, sigma, lo, hi)[0])
+        n = min(n, seq_len - used)
+        out.append(n)
+        used += n
+    return out
+
+
+@dataclass
+class PackBatch:
+    """Model-ready tensors of one or more packs, [B, S] each (dataset.py:67-76)."""
+
+    input_ids: torch.Tensor
+    labels: torch.Tensor
+    position_ids: torch.Tensor
+    doc_ids: torch.Tensor
+    doc_lengths: list[list[int]]
+
+    @property
+    def useful_tokens(self) -> int:
+        return int(sum(sum(d) for d in self.doc_lengths))
+
+    def to(self, device) -> "PackBatch":
+        return PackBatch(self.input_ids.to(device), self.labels.to(device),
+                         self.position_ids.to(device), self.doc_ids.to(device), self.doc_lengths)
+
+
+def pack_tensors(packs: list[list[int]], seq_len: int, vocab: int,
+                 rng: np.random.Generator, pad_token_id: int = 0) -> PackBatch:
+    B = len(packs)
+    input_ids = np.full((B, seq_len), pad_token_id, dtype=np.int64)
+    labels = np.full((B, seq_len), -100, dtype=np.int64)
+    position_ids = np.zeros((B, seq_len), dtype=np.int64)
+    doc_ids = np.full((B, seq_len), -1, dtype=np.int64)
+    for b, docs in enumerate(packs):
+        off = 0
+        for d, n in enumerate(docs):
+            toks = rng.integers(0, vocab, size=n, dtype=np.int64)
+            input_ids[b, off : off + n] = toks
+            if n > 1:
+                labels[b, off : off + n - 1] = toks[1:]
+            position_ids[b, off : off + n] = np.arange(n)
+            doc_ids[b, off : off + n] = d
+            off += n
+        if off > seq_len:
+            raise ValueError(f"pack {b} overflows seq_len: {off}")
+    return PackBatch(torch.from_numpy(input_ids), torch.from_numpy(labels),
+                     torch.from_numpy(position_ids), torch.from_numpy(doc_ids),
+                     [list(p) for p in packs])
+
+
+def doc_ids_from_lengths(packs: list[list[int]], seq_len: int) -> torch.Tensor:
+    out = torch.full((len(packs), seq_len), -1, dtype=torch.int64)
+    for b, docs in enumerate(packs):
+        off = 0
+        for d, n in enumerate(docs):
+            out[b, off : off + n] = d
+            off += n
+    return out
+
+
+# ---------------------------------------------------------------- configurations
+def cfg1_packs(seed: int = 0) -> list[list[int]]:
+    """4 packs of 256: lognormal(ln 48, 0.8) clipped [4, 256], BFD, seeded pick."""
+    rng = np.random.default_rng(seed)
+    lengths = lognormal_lengths(rng, 400, np.log(48), 0.8, 4, 256)
+    bins = best_fit_decreasing(lengths, 256)
+    pick = rng.permutation(len(bins))[:4]
+    return [bins[i] for i in pick]
+
+
+def cfg2_pack_pool(seed: int = 0, n_docs: int = 3000) -> list[list[int]]:
+    """BFD packs of 2048: lognormal(ln 200, 1.1) clipped [8, 2048]."""
+    rng = np.random.default_rng(seed)
+    lengths = lognormal_lengths(rng, n_docs, np.log(200), 1.1, 8, 2048)
+    return best_fit_decreasing(lengths, 2048)
+
+
+def cfg2_steps(n_steps: int, packs_per_step: int = 4, seed: int = 0) -> list[list[list[int]]]:
+    """Per-step pack lists drawn from the BFD pool by a seeded permutation."""
+    pool = cfg2_pack_pool(seed)
+    rng = np.random.default_rng(seed + 1)
+    order = rng.permutation(len(pool))
+    need = n_steps * packs_per_step
+    if need > len(order):
+        order = np.concatenate([order] * (need // len(order) + 1))
+    return [[pool[i] for i in order[s * packs_per_step : (s + 1) * packs_per_step]]
+            for s in range(n_steps)]
+
+
+def cfg3_packs(seed: int = 0) -> list[list[int]]:
+    """8 packs of 8192: pack 0 one dense document, packs 1-7 lognormal(ln 512, 1.0)."""
+    rng = np.random.default_rng(seed)
+    packs = [[8192]]
+    for _ in range(7):
+        packs.append(fill_sequential(rng, 8192, np.log(512), 1.0, 16, 8192))
+    return packs

@@ -1,0 +1,85 @@
+"""GPU parity: document block tables are bit-exact.
+
+Checked against (a) the golden fixtures produced by torch's
+create_block_mask, and (b) the numpy oracle on the benchmark workloads
+(cfg1 / cfg2 / cfg3 packs), including B > 1 through ``doc_block_tables``.
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import block_mask as OB
+from packbalance_amd.data import workloads as W
+from packbalance_amd.model.attention import build_doc_block_mask, doc_block_tables
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "block_masks.npz"
+
+
+def _assert_tables(bm_tables: dict, want: dict, what: str) -> None:
+    for name in OB.TABLE_NAMES:
+        got = bm_tables[name]
+        got = got.cpu().numpy() if isinstance(got, torch.Tensor) else got
+        assert got.dtype == np.int32, f"{what}:{name} dtype {got.dtype}"
+        np.testing.assert_array_equal(got, want[name], err_msg=f"{what}:{name}")
+
+
+def test_block_tables_match_torch_golden(dev) -> None:
+    z = np.load(GOLDEN)
+    for name in z["layouts"]:
+        name = str(name)
+        doc = torch.from_numpy(z[f"{name}/doc_ids"]).to(dev)
+        heads = int(z[f"{name}/heads"])
+        bm = build_doc_block_mask(doc[None], heads)
+        assert bm.BLOCK_SIZE == (int(z[f"{name}/block"]),) * 2, name
+        assert bm.seq_lengths == (doc.numel(), doc.numel())
+        _assert_tables({n: getattr(bm, n) for n in OB.TABLE_NAMES},
+                       {n: z[f"{name}/{n}"] for n in OB.TABLE_NAMES}, name)
+
+
+@pytest.mark.parametrize("cfg", ["cfg1", "cfg2", "cfg3"])
+def test_block_tables_on_benchmark_packs(cfg, dev) -> None:
+    if cfg == "cfg1":
+        packs, s, heads = W.cfg1_packs(), 256, 4
+    elif cfg == "cfg2":
+        packs, s, heads = W.cfg2_steps(2)[1], 2048, 12
+    else:
+        packs, s, heads = W.cfg3_packs(), 8192, 32
+    docs = W.doc_ids_from_lengths(packs, s)
+    block = OB.doc_block_size(s)
+    # Per pack through the reference entry point (B = 1).
+    for b in range(len(packs)):
+        bm = build_doc_block_mask(docs[b : b + 1].to(dev), heads)
+        want = OB.tables_closed(docs[b].numpy(), heads, block)
+        _assert_tables({n: getattr(bm, n) for n in OB.TABLE_NAMES}, want, f"{cfg}[{b}]")
+    # All packs at once (B > 1 extension).
+    t = doc_block_tables(docs.to(dev), heads, block)
+    for b in range(len(packs)):
+        want = OB.tables_closed(docs[b].numpy(), heads, block)
+        _assert_tables({n: t[n][b : b + 1] for n in OB.TABLE_NAMES}, want, f"{cfg}[B={b}]")
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_block_tables_random_layouts(seed, dev) -> None:
+    rng = np.random.default_rng(100 + seed)
+    s = int(rng.integers(1, 3000))
+    doc = np.sort(rng.integers(0, max(1, s // 50), s))
+    if seed % 2:
+        doc = rng.permutation(doc)
+    if seed >= 2 and s > 8:
+        doc[-int(rng.integers(1, 8)):] = -1
+    bm = build_doc_block_mask(torch.from_numpy(doc).to(dev), 3)
+    block = bm.BLOCK_SIZE[0]
+    want = OB.tables_dense(doc, 3, block)
+    _assert_tables({n: getattr(bm, n) for n in OB.TABLE_NAMES}, want, f"seed{seed}")
+
+
+def test_build_doc_block_mask_rejects_batch(dev) -> None:
+    with pytest.raises(ValueError):
+        build_doc_block_mask(torch.zeros(2, 64, dtype=torch.long, device=dev), 2)

@@ -1,0 +1,53 @@
+"""The C-ABI library loads and exports every symbol include/*.h declares (CPU only)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+from packbalance_amd import _native as N
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared() -> set[str]:
+    names: set[str] = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = h.read_text()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names |= set(re.findall(r"\b(pb_[a-z0-9_]+)\s*\(", text))
+    return names
+
+
+def test_library_loads() -> None:
+    assert N.available(), N._load_error
+    assert N.lib().pb_abi_version() == N.ABI_VERSION
+
+
+def test_every_declared_symbol_is_exported_and_bound() -> None:
+    declared = _declared()
+    assert {"pb_rmsnorm_fwd", "pb_swiglu_fwd", "pb_ce_rows", "pb_doc_block_tables"} <= declared
+    lib = ctypes.CDLL(str(N.LIB_PATH))
+    missing = [n for n in sorted(declared) if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+    unbound = sorted(declared - set(N.SIGNATURES))
+    assert not unbound, f"declared but without a ctypes signature: {unbound}"
+    extra = sorted(set(N.SIGNATURES) - declared)
+    assert not extra, f"bound but not declared in include/: {extra}"
+
+
+def test_status_and_error_message_without_gpu() -> None:
+    # Argument validation runs on the host before any HIP call.
+    lib = N.lib()
+    rc = lib.pb_swiglu_fwd(None, None, None, 16, 99, None)
+    assert rc == N.PB_EINVAL
+    assert b"dtype" in lib.pb_last_error()
+    rc = lib.pb_rmsnorm_fwd(None, 70000, 0, None, 0, None, 70000, None, 4, 70000, 1e-5, None)
+    assert rc == N.PB_EUNSUPPORTED
+
+
+def test_workspace_query_is_host_only() -> None:
+    lib = N.lib()
+    assert lib.pb_rmsnorm_bwd_workspace_bytes(0, 16) == 0
+    assert lib.pb_rmsnorm_bwd_workspace_bytes(32768, 4096) > 0

@@ -1,0 +1,169 @@
+"""GPU parity: RMSNorm and SwiGLU kernels vs the CPU oracle.
+
+Tolerances (torch.testing semantics, |a-b| <= atol + rtol*|b|):
+  fp32 activations: 1e-5;  bf16 activations: 1e-2 (the hot-path bar for
+  RMSNorm and SwiGLU).  The reference's own GPU test uses 2e-2
+  (tests/test_kernels.py:107-142).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import kernels as OK
+from packbalance_amd.kernels.rmsnorm import rmsnorm
+from packbalance_amd.kernels.swiglu import swiglu
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-5, torch.bfloat16: 1e-2, torch.float16: 1e-2}
+
+
+def _close(got: torch.Tensor, want: torch.Tensor, tol: float, what: str) -> None:
+    torch.testing.assert_close(got.detach().cpu().double(), want.double(), rtol=tol, atol=tol,
+                               msg=lambda m: f"{what}: {m}")
+
+
+def _rms_case(shape, dtype, wdtype, dev, *, seed=0, row_view=False, wstd=1.0, wmean=0.0):
+    g = torch.Generator().manual_seed(seed)
+    n = shape[-1]
+    if row_view:
+        base = torch.randn(*shape[:-1], n + 24, generator=g)
+        x = base.to(dev, dtype)[..., 5 : 5 + n]
+    else:
+        x = torch.randn(*shape, generator=g).to(dev, dtype)
+    w = (torch.randn(n, generator=g) * wstd + wmean).to(dev, wdtype)
+    dy = torch.randn(*shape, generator=g).to(dev, dtype)
+    return x, w, dy
+
+
+@pytest.mark.parametrize(
+    "shape,dtype,wdtype",
+    [
+        ((32, 64), torch.float32, torch.float32),  # reference GPU test shape
+        ((8, 32), torch.float32, torch.float32),
+        ((2048, 768), torch.float32, torch.float32),  # model dtype flow (fp32 residual)
+        ((4, 7, 768), torch.bfloat16, torch.float32),
+        ((513, 4096), torch.bfloat16, torch.bfloat16),
+        ((64, 100), torch.float32, torch.float32),  # n not a multiple of the vector
+        ((33, 8192), torch.bfloat16, torch.bfloat16),  # streaming (non-register) rows
+        ((16, 96), torch.float16, torch.float32),
+    ],
+)
+def test_rmsnorm_matches_oracle(shape, dtype, wdtype, dev) -> None:
+    eps = 1e-5
+    x, w, dy = _rms_case(shape, dtype, wdtype, dev)
+    xr = x.clone().requires_grad_(True)
+    wr = w.clone().requires_grad_(True)
+    y = rmsnorm(xr, wr, eps)
+    y.backward(dy)
+    tol = TOL[dtype]
+    y_ref, _ = OK.rmsnorm_fwd(x, w, eps)
+    dx_ref, dw_ref = OK.rmsnorm_bwd(dy, x, w, eps)
+    assert y.dtype == dtype and y.shape == x.shape
+    assert xr.grad.dtype == dtype and wr.grad.dtype == wdtype
+    _close(y, y_ref, tol, "y")
+    _close(xr.grad, dx_ref, tol, "dx")
+    # dw sums over all rows; compare relative to its scale.
+    _close(wr.grad, dw_ref, max(tol, 1e-4), "dw")
+
+
+def test_rmsnorm_strided_rows(dev) -> None:
+    # Rows of a wider buffer (row stride 280, base offset 20 bytes).
+    x, w, dy = _rms_case((64, 256), torch.float32, torch.float32, dev, row_view=True)
+    assert not x.is_contiguous()
+    xr = x.detach().requires_grad_(True)
+    y = rmsnorm(xr, w, 1e-5)
+    y.backward(dy)
+    _close(y, OK.rmsnorm_fwd(x, w, 1e-5)[0], 1e-5, "y (strided)")
+    _close(xr.grad, OK.rmsnorm_bwd(dy, x, w, 1e-5)[0], 1e-5, "dx (strided)")
+
+
+def test_rmsnorm_cfg5_full_size(dev) -> None:
+    """cfg5: x [32768, 4096] bf16 ~N(0,1), w ~N(1, 0.1), eps 1e-5, dy ~N(0,1).
+
+    y and dx are row-local: checked on 512 sampled rows against the fp64
+    oracle; dw (a sum over every row) is checked in full.
+    """
+    eps = 1e-5
+    x, w, dy = _rms_case((32768, 4096), torch.bfloat16, torch.bfloat16, dev, wstd=0.1, wmean=1.0)
+    xr = x.clone().requires_grad_(True)
+    wr = w.clone().requires_grad_(True)
+    y = rmsnorm(xr, wr, eps)
+    y.backward(dy)
+    rows = torch.randperm(32768, generator=torch.Generator().manual_seed(5))[:512]
+    rd = rows.to(dev)
+    _close(y[rd], OK.rmsnorm_fwd(x[rd], w, eps)[0], 1e-2, "y")
+    _close(xr.grad[rd], OK.rmsnorm_bwd(dy[rd], x[rd], w, eps)[0], 1e-2, "dx")
+    _, dw_ref = OK.rmsnorm_bwd(dy, x, w, eps)
+    _close(wr.grad, dw_ref, 1e-2, "dw")
+
+
+def test_rmsnorm_rejects_cpu_and_huge() -> None:
+    with pytest.raises(RuntimeError):
+        rmsnorm(torch.randn(2, 8), torch.ones(8), 1e-5)
+    with pytest.raises(RuntimeError):
+        rmsnorm(torch.randn(1, 70000, device="cuda"), torch.ones(70000, device="cuda"), 1e-5)
+
+
+@pytest.mark.parametrize(
+    "shape,dtype",
+    [
+        ((16, 32), torch.float32),  # reference GPU test shape
+        ((8, 16), torch.float32),
+        ((1, 2048, 2048), torch.bfloat16),  # model call site
+        ((7, 333), torch.bfloat16),  # scalar tail
+        ((5, 64), torch.float16),
+    ],
+)
+def test_swiglu_matches_oracle(shape, dtype, dev) -> None:
+    g0 = torch.Generator().manual_seed(0)
+    gate = torch.randn(*shape, generator=g0).to(dev, dtype)
+    up = torch.randn(*shape, generator=g0).to(dev, dtype)
+    dy = torch.randn(*shape, generator=g0).to(dev, dtype)
+    gr = gate.clone().requires_grad_(True)
+    ur = up.clone().requires_grad_(True)
+    out = swiglu(gr, ur)
+    out.backward(dy)
+    tol = TOL[dtype]
+    _close(out, OK.swiglu_fwd(gate, up), tol, "out")
+    dg, du = OK.swiglu_bwd(gate, up, dy)
+    _close(gr.grad, dg, tol, "dgate")
+    _close(ur.grad, du, tol, "dup")
+
+
+def test_swiglu_cfg5_full_size(dev) -> None:
+    """cfg5: gate/up [32768, 14336] bf16 ~N(0,1), dy ~N(0,1).
+
+    1M sampled elements against the fp64 oracle, every element against a
+    torch fp32 evaluation of the same formula on the device.
+    """
+    torch.manual_seed(0)
+    shape = (32768, 14336)
+    gate = torch.randn(shape, device=dev, dtype=torch.bfloat16)
+    up = torch.randn(shape, device=dev, dtype=torch.bfloat16)
+    dy = torch.randn(shape, device=dev, dtype=torch.bfloat16)
+    gr = gate.clone().requires_grad_(True)
+    ur = up.clone().requires_grad_(True)
+    out = swiglu(gr, ur)
+    out.backward(dy)
+    idx = torch.randint(0, gate.numel(), (1 << 20,), device=dev)
+    gf, uf, df = (t.reshape(-1)[idx] for t in (gate, up, dy))
+    _close(out.reshape(-1)[idx], OK.swiglu_fwd(gf, uf), 1e-2, "out (sampled)")
+    dg, du = OK.swiglu_bwd(gf, uf, df)
+    _close(gr.grad.reshape(-1)[idx], dg, 1e-2, "dgate (sampled)")
+    _close(ur.grad.reshape(-1)[idx], du, 1e-2, "dup (sampled)")
+    # Whole tensors against torch fp32, chunked to bound memory.
+    for r in range(0, shape[0], 4096):
+        g, u, d = (t[r : r + 4096].float() for t in (gate, up, dy))
+        s = torch.sigmoid(g)
+        torch.testing.assert_close(out[r : r + 4096].float(), g * s * u, rtol=1e-2, atol=1e-2)
+        torch.testing.assert_close(gr.grad[r : r + 4096].float(), d * u * s * (1 + g * (1 - s)),
+                                   rtol=1e-2, atol=1e-2)
+        torch.testing.assert_close(ur.grad[r : r + 4096].float(), d * g * s, rtol=1e-2, atol=1e-2)
+
+
+def test_swiglu_rejects_cpu() -> None:
+    with pytest.raises(RuntimeError):
+        swiglu(torch.randn(4), torch.randn(4))

@@ -1,0 +1,212 @@
+"""Pins for the CPU oracle (runs without a GPU).
+
+Each oracle function is checked against something other than its own
+formula: a PyTorch library routine, autograd, a golden fixture produced by
+torch's create_block_mask, an independent restatement, or a closed form.
+"""
+
+from __future__ import annotations
+
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import attention as OA
+from oracle import block_mask as OB
+from oracle import kernels as OK
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "block_masks.npz"
+
+
+# ---------------------------------------------------------------- RMSNorm
+def test_rmsnorm_oracle_matches_autograd_and_closed_form() -> None:
+    torch.manual_seed(0)
+    x = torch.randn(8, 32, dtype=torch.float64)
+    w = torch.randn(32, dtype=torch.float64)
+    dy = torch.randn(8, 32, dtype=torch.float64)
+    eps = 1e-5
+    xa = x.clone().requires_grad_(True)
+    wa = w.clone().requires_grad_(True)
+    ya = xa * torch.rsqrt(xa.pow(2).mean(-1, keepdim=True) + eps) * wa
+    ya.backward(dy)
+    y, rstd = OK.rmsnorm_fwd(x, w, eps)
+    dx, dw = OK.rmsnorm_bwd(dy, x, w, eps)
+    torch.testing.assert_close(y, ya.detach(), rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(dx, xa.grad, rtol=1e-10, atol=1e-10)
+    torch.testing.assert_close(dw, wa.grad, rtol=1e-10, atol=1e-10)
+    # Closed form: a constant row c gives rstd = 1/sqrt(c^2 + eps).
+    c = torch.full((1, 16), 3.0, dtype=torch.float64)
+    _, r = OK.rmsnorm_fwd(c, torch.ones(16, dtype=torch.float64), eps)
+    assert abs(float(r[0]) - 1.0 / math.sqrt(9.0 + eps)) < 1e-15
+
+
+# ---------------------------------------------------------------- SwiGLU
+def test_swiglu_oracle_matches_autograd() -> None:
+    torch.manual_seed(0)
+    g = torch.randn(8, 16, dtype=torch.float64, requires_grad=True)
+    u = torch.randn(8, 16, dtype=torch.float64, requires_grad=True)
+    dy = torch.randn(8, 16, dtype=torch.float64)
+    ref = F.silu(g) * u
+    ref.backward(dy)
+    out = OK.swiglu_fwd(g, u)
+    dg, du = OK.swiglu_bwd(g, u, dy)
+    torch.testing.assert_close(out, ref.detach(), rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(dg, g.grad, rtol=1e-10, atol=1e-10)
+    torch.testing.assert_close(du, u.grad, rtol=1e-10, atol=1e-10)
+
+
+# ---------------------------------------------------------------- CE
+@pytest.mark.parametrize("z_loss", [0.0, 0.01])
+def test_linear_ce_oracle_matches_full_ce(z_loss: float) -> None:
+    # The reference's own CE test pattern (tests/test_kernels.py:64-81).
+    torch.manual_seed(0)
+    x = torch.randn(37, 32, dtype=torch.float64)
+    w = torch.randn(64, 32, dtype=torch.float64)
+    t = torch.randint(0, 64, (37,))
+    t[::7] = -100
+    x1 = x.clone().requires_grad_(True)
+    w1 = w.clone().requires_grad_(True)
+    loss = OK.full_ce_reference(x1, w1, t, z_loss)
+    loss.backward()
+    l2, dx, dw = OK.linear_ce(x, w, t, z_loss_coeff=z_loss)
+    # The reference formula takes the z-loss lse through .float() (fp32).
+    tol = 1e-10 if z_loss == 0 else 1e-6
+    torch.testing.assert_close(l2, loss.detach(), rtol=tol, atol=tol)
+    torch.testing.assert_close(dx, x1.grad, rtol=tol, atol=tol)
+    torch.testing.assert_close(dw, w1.grad, rtol=tol, atol=tol)
+
+
+def test_ce_rows_special_cases() -> None:
+    # Uniform logits: loss = ln V; all-ignored rows: 0; V = 1: loss 0.
+    V = 1000
+    logits = torch.zeros(3, V, dtype=torch.float64)
+    loss, lse, dl = OK.ce_rows(logits, torch.tensor([5, -100, 7]))
+    assert abs(float(loss[0]) - math.log(V)) < 1e-12
+    assert float(loss[1]) == 0.0 and float(dl[1].abs().sum()) == 0.0
+    assert abs(float(dl[0].sum())) < 1e-12  # softmax - onehot sums to 0
+    l1, _, _ = OK.ce_rows(torch.randn(4, 1, dtype=torch.float64), torch.zeros(4, dtype=torch.int64))
+    assert float(l1.abs().max()) < 1e-12
+
+
+def test_linear_ce_rejects_row_mismatch() -> None:
+    with pytest.raises(ValueError):
+        OK.linear_ce(torch.randn(4, 8), torch.randn(5, 8), torch.zeros(3, dtype=torch.int64))
+
+
+# ---------------------------------------------------------------- attention
+def test_attention_oracle_matches_sdpa_dense_mask() -> None:
+    # The reference's eager-attention test pattern (tests/test_attention.py:14-23).
+    torch.manual_seed(0)
+    q, k, v = (torch.randn(1, 2, 8, 4, dtype=torch.float64) for _ in range(3))
+    doc = torch.tensor([[0, 0, 0, 1, 1, 2, 2, 2]])
+    mask = OA.dense_mask(doc)
+    ref = F.scaled_dot_product_attention(q, k, v, attn_mask=mask[:, None])
+    out = OA.attention(q, k, v, doc)["out"]
+    torch.testing.assert_close(out, ref, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("semantics", ["flex", "eager"])
+def test_attention_oracle_grads_match_autograd_gqa(semantics: str) -> None:
+    torch.manual_seed(1)
+    B, Hq, Hkv, S, D = 2, 4, 2, 40, 8
+    q = torch.randn(B, Hq, S, D, dtype=torch.float64, requires_grad=True)
+    k = torch.randn(B, Hkv, S, D, dtype=torch.float64, requires_grad=True)
+    v = torch.randn(B, Hkv, S, D, dtype=torch.float64, requires_grad=True)
+    doc = torch.tensor([[0] * 13 + [1] * 20 + [-1] * 7, [3] * 5 + [4] * 30 + [5] * 5])
+    do = torch.randn(B, Hq, S, D, dtype=torch.float64)
+    mask = OA.dense_mask(doc)
+    if semantics == "eager":
+        mask = mask & (doc[:, :, None] >= 0) & (doc[:, None, :] >= 0)
+    ke = k.repeat_interleave(Hq // Hkv, dim=1)
+    ve = v.repeat_interleave(Hq // Hkv, dim=1)
+    s = (q @ ke.transpose(-1, -2)) / math.sqrt(D)
+    s = s.masked_fill(~mask[:, None], -math.inf)
+    p = torch.softmax(s, dim=-1)
+    p = torch.nan_to_num(p, nan=0.0)  # fully-masked eager pad rows
+    ref = p @ ve
+    ref.backward(do)
+    res = OA.attention(q, k, v, doc, do, semantics=semantics)
+    torch.testing.assert_close(res["out"], ref.detach(), rtol=1e-10, atol=1e-10)
+    torch.testing.assert_close(res["dq"], q.grad, rtol=1e-9, atol=1e-9)
+    torch.testing.assert_close(res["dk"], k.grad, rtol=1e-9, atol=1e-9)
+    torch.testing.assert_close(res["dv"], v.grad, rtol=1e-9, atol=1e-9)
+
+
+def test_attention_oracle_special_cases() -> None:
+    # Every token its own document: softmax over one key, out == v (GQA-mapped).
+    torch.manual_seed(2)
+    q = torch.randn(1, 4, 6, 8, dtype=torch.float64)
+    k = torch.randn(1, 2, 6, 8, dtype=torch.float64)
+    v = torch.randn(1, 2, 6, 8, dtype=torch.float64)
+    out = OA.attention(q, k, v, torch.arange(6)[None])["out"]
+    torch.testing.assert_close(out, v.repeat_interleave(2, dim=1), rtol=0, atol=1e-15)
+    # Identical keys: uniform causal average of the values of the document.
+    k1 = torch.zeros(1, 1, 5, 8, dtype=torch.float64)
+    v1 = torch.arange(5, dtype=torch.float64)[None, None, :, None].expand(1, 1, 5, 8)
+    o1 = OA.attention(torch.randn(1, 1, 5, 8, dtype=torch.float64), k1, v1, torch.zeros(1, 5))["out"]
+    want = torch.tensor([0.0, 0.5, 1.0, 1.5, 2.0], dtype=torch.float64)
+    torch.testing.assert_close(o1[0, 0, :, 0], want, rtol=0, atol=1e-12)
+
+
+def test_attention_flops_single_doc() -> None:
+    f = OA.attention_flops([8192], 128, 32)
+    assert f["pairs"] == 33_558_528
+    assert abs(f["fwd"] + f["bwd"] - 1.649e12) / 1.649e12 < 1e-3  # one dense 8192-token pack, Hq=32, D=128
+
+
+# ---------------------------------------------------------------- block tables
+def _golden():
+    z = np.load(GOLDEN)
+    for name in z["layouts"]:
+        yield str(name), z
+
+
+def test_block_mask_oracle_matches_torch_golden() -> None:
+    n = 0
+    for name, z in _golden():
+        doc = z[f"{name}/doc_ids"]
+        heads = int(z[f"{name}/heads"])
+        tabs, block = OB.build_doc_block_tables(doc, heads)
+        assert block == int(z[f"{name}/block"]), name
+        for t in OB.TABLE_NAMES:
+            np.testing.assert_array_equal(tabs[t], z[f"{name}/{t}"], err_msg=f"{name}:{t}")
+        # The closed-form restatement must agree too.
+        closed = OB.tables_closed(doc, heads, block)
+        for t in OB.TABLE_NAMES:
+            np.testing.assert_array_equal(closed[t], z[f"{name}/{t}"], err_msg=f"closed {name}:{t}")
+        n += 1
+    assert n >= 15
+
+
+def test_block_mask_known_answer() -> None:
+    # One document of 256 tokens (checked against torch when the fixture was made).
+    tabs, block = OB.build_doc_block_tables(np.zeros(256, dtype=np.int64), 1)
+    assert block == 128
+    assert tabs["kv_num_blocks"][0, 0].tolist() == [1, 1]
+    assert tabs["kv_indices"][0, 0].tolist() == [[0, 1], [1, 0]]
+    assert tabs["full_kv_num_blocks"][0, 0].tolist() == [0, 1]
+    assert tabs["full_kv_indices"][0, 0].tolist() == [[0, 1], [0, 1]]
+    assert tabs["full_q_num_blocks"][0, 0].tolist() == [1, 0]
+    assert tabs["full_q_indices"][0, 0].tolist() == [[1, 0], [0, 1]]
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_block_mask_dense_and_closed_agree(seed: int) -> None:
+    rng = np.random.default_rng(seed)
+    s = int(rng.integers(1, 700))
+    block = int(rng.choice([32, 64, 128]))
+    doc = np.sort(rng.integers(0, max(1, s // 20), s))
+    if seed % 2:
+        doc = rng.permutation(doc)  # non-contiguous documents
+    if seed % 3 == 0 and s > 4:
+        doc[-3:] = -1
+    np.testing.assert_array_equal(OB.classify_dense(doc, block), OB.classify_closed(doc, block))
+
+
+def test_block_mask_rejects_batch() -> None:
+    with pytest.raises(ValueError):
+        OB.build_doc_block_tables(np.zeros((2, 8), dtype=np.int64), 1)
