@@ -115,6 +115,58 @@ int pb_doc_block_tables(const int64_t *doc_ids, int64_t doc_stride, int64_t b,
                         int32_t *full_q_num, int32_t *full_q_idx,
                         uint8_t *class_ws, void *stream);
 
+/* ---- Document-masked GQA attention --------------------------------------
+ * A [B, H, S, D] tensor view: element strides for b, h, s; D is unit-stride.
+ * The model's q/k/v are .transpose(1, 2) views of [B, S, H, D] memory
+ * (packbalance/model/llama.py:86-92), so any stride order is accepted.      */
+typedef struct pb_bhsd {
+  void *data;
+  int64_t stride_b;
+  int64_t stride_h;
+  int64_t stride_s;
+} pb_bhsd;
+
+/* Tile size of an attention kernel: kernel 0 = forward, 1 = dK/dV backward,
+ * 2 = dQ backward; which 0 = query tile, 1 = key/value tile.  Plans passed to
+ * pb_attn_fwd / pb_attn_bwd must be built with these sizes.                */
+int pb_attn_tile(int kernel, int64_t head_dim, int which);
+
+/* Tile plan of a packed batch (no counterpart table in the reference; it is
+ * the kernels' form of BlockMask.{kv,full_kv}_indices (by_kv = 0) or
+ * {q,full_q}_indices (by_kv = 1) at the kernel tile sizes):
+ *   counts[b][r]            number of non-empty tiles for row tile r
+ *   lists[b][r][0..counts)  ascending tile indices, each (tile << 1) | FULL
+ * Row tiles are query tiles of q_tile tokens (by_kv = 0) or key tiles of
+ * kv_tile tokens (by_kv = 1).  class_ws holds b*nq*nkv bytes.               */
+int pb_attn_plan(const int64_t *doc_ids, int64_t doc_stride, int64_t b, int64_t s,
+                 int64_t q_tile, int64_t kv_tile, int by_kv, int32_t *counts,
+                 int32_t *lists, uint8_t *class_ws, void *stream);
+
+/* Replaces the FlexAttention forward launched at packbalance/model/attention.py:116-122
+ * (flex_attention(q, k, v, block_mask=doc mask, enable_gqa=Hq != Hkv)):
+ *   out[b,h,i] = sum_j softmax_j(scale * q[b,h,i].k[b,h/G,j] | mask) v[b,h/G,j]
+ * with mask(i, j) = doc[b,i] == doc[b,j] && i >= j, G = hq / hkv.
+ * q/k/v/out are bf16 (dtype must be PB_BF16), head_dim d <= 128.
+ * lse (fp32 [b, hq, s]) receives log2(sum_j exp2(scale*log2(e)*q.k)) for the
+ * backward.  plan = pb_attn_plan(by_kv = 0) with the kernel-0 tile sizes.   */
+int pb_attn_fwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v, const pb_bhsd *out,
+                float *lse, const int64_t *doc_ids, int64_t doc_stride,
+                const int32_t *plan_counts, const int32_t *plan_lists, int64_t b,
+                int64_t hq, int64_t hkv, int64_t s, int64_t d, float scale, int dtype,
+                void *stream);
+
+/* Replaces the FlexAttention backward (dQ, dK, dV; dK/dV summed over each
+ * GQA group, as enable_gqa does).  delta_ws is an fp32 [b, hq, s] workspace.
+ * kv_plan = pb_attn_plan(by_kv = 1) with the kernel-1 tile sizes,
+ * q_plan  = pb_attn_plan(by_kv = 0) with the kernel-2 tile sizes.           */
+int pb_attn_bwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v, const pb_bhsd *out,
+                const pb_bhsd *dout, const pb_bhsd *dq, const pb_bhsd *dk,
+                const pb_bhsd *dv, const float *lse, float *delta_ws,
+                const int64_t *doc_ids, int64_t doc_stride, const int32_t *q_plan_counts,
+                const int32_t *q_plan_lists, const int32_t *kv_plan_counts,
+                const int32_t *kv_plan_lists, int64_t b, int64_t hq, int64_t hkv, int64_t s,
+                int64_t d, float scale, int dtype, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -30,7 +30,7 @@ def _chunk_rows(heads: int, keys: int, budget_bytes: int = 1 << 27) -> int:
 
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, doc_ids: torch.Tensor,
               dout: torch.Tensor | None = None, *, semantics: str = "flex",
-              scale: float | None = None):
+              scale: float | None = None, dtype: torch.dtype = torch.float64):
     """Document-masked causal GQA attention in float64.
 
     q [B, Hq, S, D], k/v [B, Hkv, S, D], doc_ids [B, S] (int), dout like q.
@@ -38,7 +38,8 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, doc_ids: torch.
                "eager" -> eager_attention of attention.py:66-95 (pad rows are 0
                           and never attend or get attended).
     Returns dict with out [B,Hq,S,D], lse [B,Hq,S] (natural log; -inf on rows
-    with no allowed key) and, if dout is given, dq, dk, dv (float64, CPU).
+    with no allowed key) and, if dout is given, dq, dk, dv (CPU, ``dtype``;
+    float64 unless a caller trades precision for speed on large packs).
     """
     if semantics not in ("flex", "eager"):
         raise ValueError(semantics)
@@ -49,16 +50,16 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, doc_ids: torch.
     G = Hq // Hkv
     sc = 1.0 / math.sqrt(D) if scale is None else scale
     dev = "cpu"
-    Q = q.detach().to(dev, torch.float64)
-    K = k.detach().to(dev, torch.float64).repeat_interleave(G, dim=1)
-    V = v.detach().to(dev, torch.float64).repeat_interleave(G, dim=1)
-    dO = None if dout is None else dout.detach().to(dev, torch.float64)
+    Q = q.detach().to(dev, dtype)
+    K = k.detach().to(dev, dtype).repeat_interleave(G, dim=1)
+    V = v.detach().to(dev, dtype).repeat_interleave(G, dim=1)
+    dO = None if dout is None else dout.detach().to(dev, dtype)
     docs = doc_ids.detach().to(dev, torch.int64).reshape(B, S)
 
-    out = torch.zeros(B, Hq, S, D, dtype=torch.float64)
-    lse = torch.full((B, Hq, S), -math.inf, dtype=torch.float64)
+    out = torch.zeros(B, Hq, S, D, dtype=dtype)
+    lse = torch.full((B, Hq, S), -math.inf, dtype=dtype)
     dq = torch.zeros_like(out) if dO is not None else None
-    dk_full = torch.zeros(B, Hq, S, D, dtype=torch.float64) if dO is not None else None
+    dk_full = torch.zeros(B, Hq, S, D, dtype=dtype) if dO is not None else None
     dv_full = torch.zeros_like(dk_full) if dO is not None else None
 
     pos = torch.arange(S)

@@ -34,6 +34,22 @@ _i64 = C.c_int64
 _i32 = C.c_int
 _f32 = C.c_float
 
+
+class BHSD(C.Structure):
+    """``pb_bhsd``: a [B, H, S, D] view (element strides; D has unit stride)."""
+
+    _fields_ = [("data", C.c_void_p), ("stride_b", C.c_int64), ("stride_h", C.c_int64),
+                ("stride_s", C.c_int64)]
+
+    @classmethod
+    def of(cls, t: torch.Tensor) -> "BHSD":
+        if t.dim() != 4 or t.stride(-1) != 1:
+            raise ValueError("expected a [B, H, S, D] tensor with unit stride on D")
+        return cls(t.data_ptr(), t.stride(0), t.stride(1), t.stride(2))
+
+
+_pv = C.POINTER(BHSD)
+
 # name -> (restype, argtypes).  Kept in the order of the header.
 SIGNATURES: dict[str, tuple] = {
     "pb_last_error": (C.c_char_p, []),
@@ -50,6 +66,17 @@ SIGNATURES: dict[str, tuple] = {
     "pb_doc_block_tables": (
         _i32,
         [_p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p],
+    ),
+    "pb_attn_tile": (_i32, [_i32, _i64, _i32]),
+    "pb_attn_plan": (_i32, [_p, _i64, _i64, _i64, _i64, _i64, _i32, _p, _p, _p, _p]),
+    "pb_attn_fwd": (
+        _i32,
+        [_pv, _pv, _pv, _pv, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _p],
+    ),
+    "pb_attn_bwd": (
+        _i32,
+        [_pv, _pv, _pv, _pv, _pv, _pv, _pv, _pv, _p, _p, _p, _i64, _p, _p, _p, _p,
+         _i64, _i64, _i64, _i64, _i64, _f32, _i32, _p],
     ),
 }
 

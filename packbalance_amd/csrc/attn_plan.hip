@@ -1,0 +1,54 @@
+// Tile plans for the document-masked attention kernels.
+//
+// A plan lists, for every row tile of one orientation, the non-empty tiles of
+// the other orientation in ascending order, each tagged FULL (no element mask
+// needed) or PARTIAL.  It is the attention kernels' form of the FlexAttention
+// block tables (kv_indices / full_kv_indices for by_kv = 0, q_indices /
+// full_q_indices for by_kv = 1), at the kernels' own tile sizes, with FULL and
+// PARTIAL merged into one ascending list so a kernel walks one array.
+#include "attn_common.hpp"
+
+namespace pb {
+namespace {
+
+enum : uint8_t { kEmpty = 0, kPartial = 1, kFull = 2 };
+
+__global__ __launch_bounds__(256) void plan_lists(const uint8_t *__restrict__ cls, int nb, int nq,
+                                                  int nk, int by_kv, int32_t *__restrict__ counts,
+                                                  int32_t *__restrict__ lists) {
+  const int nrows = by_kv ? nk : nq, ncols = by_kv ? nq : nk;
+  const int64_t tid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (tid >= (int64_t)nb * nrows) return;
+  const int b = (int)(tid / nrows), r = (int)(tid - (int64_t)b * nrows);
+  const uint8_t *C = cls + (int64_t)b * nq * nk;
+  int32_t *L = lists + tid * ncols;
+  int n = 0;
+  for (int c = 0; c < ncols; ++c) {
+    const uint8_t v = by_kv ? C[(int64_t)c * nk + r] : C[(int64_t)r * nk + c];
+    if (v != kEmpty) L[n++] = (c << 1) | (v == kFull ? 1 : 0);
+  }
+  counts[tid] = n;
+}
+
+}  // namespace
+}  // namespace pb
+
+extern "C" int pb_attn_plan(const int64_t *doc_ids, int64_t doc_stride, int64_t b, int64_t s,
+                            int64_t q_tile, int64_t kv_tile, int by_kv, int32_t *counts,
+                            int32_t *lists, uint8_t *class_ws, void *stream) {
+  using namespace pb;
+  clear_error();
+  PB_CHECK_ARG(b >= 1 && s >= 1, "pb_attn_plan: bad shape b=%lld s=%lld", (long long)b, (long long)s);
+  PB_CHECK_ARG(q_tile >= 1 && q_tile <= 1024 && kv_tile >= 1 && kv_tile <= 1024,
+               "pb_attn_plan: tile sizes out of [1, 1024]");
+  PB_CHECK_ARG(doc_stride >= s, "pb_attn_plan: doc_stride < s");
+  PB_CHECK_ARG(by_kv == 0 || by_kv == 1, "pb_attn_plan: by_kv must be 0 or 1");
+  hipStream_t st = as_stream(stream);
+  int rc = classify_doc_tiles(doc_ids, doc_stride, b, s, (int)q_tile, (int)kv_tile, class_ws, st);
+  if (rc) return rc;
+  const int nq = (int)((s + q_tile - 1) / q_tile), nk = (int)((s + kv_tile - 1) / kv_tile);
+  const int64_t rows = b * (by_kv ? nk : nq);
+  hipLaunchKernelGGL(plan_lists, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st, class_ws,
+                     (int)b, nq, nk, by_kv, counts, lists);
+  return launch_status("pb_attn_plan");
+}

@@ -37,10 +37,6 @@ except ImportError:  # pragma: no cover - torch without FlexAttention
 
 HAS_NATIVE = N.available()
 
-# The reference module exports these two names; ``flex_attention`` here is the
-# native kernel with FlexAttention's calling convention for this mask.
-create_block_mask = None
-
 
 def _block_size(seq_len: int, block_size: int) -> int:
     # attention.py:40-41: never below 32, a power of two, at most block_size.
@@ -122,6 +118,159 @@ def build_doc_block_mask(doc_ids: torch.Tensor, n_heads: int, block_size: int = 
         t["q_num_blocks"], t["q_indices"], t["full_q_num_blocks"], t["full_q_indices"],
         (block, block), mask_mod, doc_ids=ids,
     )
+
+
+# ---------------------------------------------------------------- native attention
+FWD, BWD_KV, BWD_Q = 0, 1, 2
+
+
+class _Plan:
+    """Tile plan of a packed batch for one kernel (see ``pb_attn_plan``)."""
+
+    def __init__(self, doc: torch.Tensor, kernel: int, head_dim: int):
+        lib = N.lib()
+        self.q_tile = lib.pb_attn_tile(kernel, head_dim, 0)
+        self.kv_tile = lib.pb_attn_tile(kernel, head_dim, 1)
+        by_kv = 1 if kernel == BWD_KV else 0
+        b, s = doc.shape
+        nq = -(-s // self.q_tile)
+        nk = -(-s // self.kv_tile)
+        rows, cols = (nk, nq) if by_kv else (nq, nk)
+        dev = doc.device
+        self.counts = torch.empty((b, rows), dtype=torch.int32, device=dev)
+        self.lists = torch.empty((b, rows, cols), dtype=torch.int32, device=dev)
+        ws = torch.empty(b * nq * nk, dtype=torch.uint8, device=dev)
+        N.call("pb_attn_plan", doc.data_ptr(), doc.stride(0), b, s, self.q_tile, self.kv_tile,
+               by_kv, self.counts.data_ptr(), self.lists.data_ptr(), ws.data_ptr(),
+               N.stream_ptr(doc))
+
+
+def _doc_2d(doc_ids: torch.Tensor, batch: int, seq_len: int) -> torch.Tensor:
+    d = doc_ids.to(torch.int64)
+    if d.dim() == 1:
+        d = d[None]
+    if d.shape[-1] != seq_len or d.shape[0] not in (1, batch):
+        raise ValueError(f"doc_ids shape {tuple(doc_ids.shape)} does not match [B={batch}, S={seq_len}]")
+    if d.shape[0] != batch:
+        d = d.expand(batch, seq_len)
+    return d.contiguous()
+
+
+def _plans(doc: torch.Tensor, head_dim: int, block_mask) -> dict:
+    """Plans for the three kernels; cached on a DocBlockMask built from the same doc_ids."""
+    # The model passes the very doc_ids tensor the mask was built from; the
+    # mask keeps it alive, so pointer identity is a sync-free cache key.
+    cache = None
+    if (isinstance(block_mask, DocBlockMask) and block_mask.doc_ids.shape == doc.shape
+            and block_mask.doc_ids.data_ptr() == doc.data_ptr()):
+        cache = block_mask._plans
+    key = ("plans", head_dim)
+    if cache is not None and key in cache:
+        return cache[key]
+    plans = {k: _Plan(doc, k, head_dim) for k in (FWD, BWD_KV, BWD_Q)}
+    if cache is not None:
+        cache[key] = plans
+    return plans
+
+
+class _DocAttention(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, doc, plans, scale):
+        B, Hq, S, D = q.shape
+        Hkv = k.shape[1]
+        out_mem = torch.empty((B, S, Hq, D), dtype=q.dtype, device=q.device)
+        out = out_mem.transpose(1, 2)
+        lse = torch.empty((B, Hq, S), dtype=torch.float32, device=q.device)
+        p = plans[FWD]
+        N.call("pb_attn_fwd", N.BHSD.of(q), N.BHSD.of(k), N.BHSD.of(v), N.BHSD.of(out),
+               lse.data_ptr(), doc.data_ptr(), doc.stride(0), p.counts.data_ptr(),
+               p.lists.data_ptr(), B, Hq, Hkv, S, D, float(scale), N.PB_BF16, N.stream_ptr(q))
+        ctx.save_for_backward(q, k, v, out, lse, doc)
+        ctx.plans = plans
+        ctx.scale = scale
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, out, lse, doc = ctx.saved_tensors
+        B, Hq, S, D = q.shape
+        Hkv = k.shape[1]
+        g = dout.to(torch.bfloat16)
+        if g.stride(-1) != 1:
+            g = g.contiguous()
+        dq = torch.empty((B, S, Hq, D), dtype=q.dtype, device=q.device).transpose(1, 2)
+        dk = torch.empty((B, S, Hkv, D), dtype=k.dtype, device=k.device).transpose(1, 2)
+        dv = torch.empty((B, S, Hkv, D), dtype=v.dtype, device=v.device).transpose(1, 2)
+        delta = torch.empty((B, Hq, S), dtype=torch.float32, device=q.device)
+        pq, pkv = ctx.plans[BWD_Q], ctx.plans[BWD_KV]
+        N.call("pb_attn_bwd", N.BHSD.of(q), N.BHSD.of(k), N.BHSD.of(v), N.BHSD.of(out),
+               N.BHSD.of(g), N.BHSD.of(dq), N.BHSD.of(dk), N.BHSD.of(dv), lse.data_ptr(),
+               delta.data_ptr(), doc.data_ptr(), doc.stride(0), pq.counts.data_ptr(),
+               pq.lists.data_ptr(), pkv.counts.data_ptr(), pkv.lists.data_ptr(),
+               B, Hq, Hkv, S, D, float(ctx.scale), N.PB_BF16, N.stream_ptr(q))
+        return dq, dk, dv, None, None, None
+
+
+def _bhsd(t: torch.Tensor) -> torch.Tensor:
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
+def doc_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, doc_ids: torch.Tensor,
+                  *, block_mask=None, scale: float | None = None) -> torch.Tensor:
+    """Document-masked causal GQA attention on the gfx950 kernels.
+
+    q [B, Hq, S, D], k/v [B, Hkv, S, D] (any strides with unit D stride),
+    doc_ids [B, S] or [S].  bf16 operands with fp32 accumulation; other
+    floating dtypes are computed with bf16 operands and returned in their own
+    dtype.  Returns [B, Hq, S, D] (a transposed view of [B, S, Hq, D] memory).
+    """
+    N.require_device(q, k, v, doc_ids, op="attention_forward")
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k, v must be [B, H, S, D]")
+    B, Hq, S, D = q.shape
+    if k.shape != v.shape or k.shape[0] != B or k.shape[2] != S or k.shape[3] != D:
+        raise ValueError(f"k {tuple(k.shape)} / v {tuple(v.shape)} do not match q {tuple(q.shape)}")
+    if Hq % k.shape[1]:
+        raise ValueError("query heads must be a multiple of key/value heads")
+    if D > 128:
+        raise RuntimeError(f"head_dim {D} > 128 is not supported by the attention kernels")
+    doc = _doc_2d(doc_ids, B, S)
+    plans = _plans(doc, D, block_mask)
+    sc = (1.0 / D ** 0.5) if scale is None else float(scale)
+    dtype = q.dtype
+    qb, kb, vb = (_bhsd(t.to(torch.bfloat16)) for t in (q, k, v))
+    out = _DocAttention.apply(qb, kb, vb, doc, plans, sc)
+    return out if dtype == torch.bfloat16 else out.to(dtype)
+
+
+def flex_attention(query, key, value, block_mask=None, enable_gqa: bool = False, scale=None):
+    """FlexAttention-style entry for the document mask (reference test calling convention).
+
+    ``block_mask`` must be a mask from :func:`build_doc_block_mask`; its doc_ids
+    define the mask.
+    """
+    if not isinstance(block_mask, DocBlockMask):
+        raise ValueError("flex_attention here needs the BlockMask of build_doc_block_mask")
+    if query.shape[1] != key.shape[1] and not enable_gqa:
+        raise ValueError("query and key heads differ; pass enable_gqa=True")
+    return doc_attention(query, key, value, block_mask.doc_ids, block_mask=block_mask, scale=scale)
+
+
+def attention_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, doc_ids: torch.Tensor,
+                      *, block_mask=None, backend: str = "auto",
+                      compile_attention: bool = True) -> torch.Tensor:
+    """Reference dispatch (attention.py:98-125) onto the native kernels.
+
+    "auto" and "flex" run the gfx950 kernels (CPU tensors raise); "eager" runs
+    the per-document SDPA loop; anything else raises ValueError.
+    ``compile_attention`` is accepted for API compatibility.
+    """
+    del compile_attention
+    if backend in ("auto", "flex"):
+        return doc_attention(q, k, v, doc_ids, block_mask=block_mask)
+    if backend == "eager":
+        return eager_attention(q, k, v, doc_ids)
+    raise ValueError(f"unknown attention backend {backend}")
 
 
 def eager_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,

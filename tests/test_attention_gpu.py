@@ -1,0 +1,169 @@
+"""GPU parity: document-masked GQA attention forward and backward vs the oracle.
+
+Tolerance: outputs and gradients within 2e-2 absolute (plus 2e-2 relative for
+entries above 1, where bf16 storage itself rounds by more than 2e-2), bf16
+operands with fp32 accumulation, against the float64 oracle on the same
+bf16 inputs.  Padding rows (doc_id -1) follow FlexAttention's mask_mod
+semantics (a pad attends to earlier pads); the eager convention (pad rows 0)
+is checked separately on real rows.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from oracle import attention as OA
+from packbalance_amd.data import workloads as W
+from packbalance_amd.model.attention import (
+    attention_forward,
+    build_doc_block_mask,
+    doc_attention,
+    flex_attention,
+)
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-2
+
+
+def _close(got, want, what):
+    torch.testing.assert_close(got.detach().float().cpu(), want.float(), atol=TOL, rtol=TOL,
+                               msg=lambda m: f"{what}: {m}")
+
+
+def _inputs(B, Hq, Hkv, S, D, dev, *, seed=0, model_layout=True):
+    """q/k/v as the model makes them: .transpose(1, 2) views of [B, S, H, D] memory."""
+    g = torch.Generator().manual_seed(seed)
+    if model_layout:
+        q = torch.randn(B, S, Hq, D, generator=g).to(dev, torch.bfloat16).transpose(1, 2)
+        k = torch.randn(B, S, Hkv, D, generator=g).to(dev, torch.bfloat16).transpose(1, 2)
+        v = torch.randn(B, S, Hkv, D, generator=g).to(dev, torch.bfloat16).transpose(1, 2)
+        do = torch.randn(B, S, Hq, D, generator=g).to(dev, torch.bfloat16).transpose(1, 2)
+    else:
+        q = torch.randn(B, Hq, S, D, generator=g).to(dev, torch.bfloat16)
+        k = torch.randn(B, Hkv, S, D, generator=g).to(dev, torch.bfloat16)
+        v = torch.randn(B, Hkv, S, D, generator=g).to(dev, torch.bfloat16)
+        do = torch.randn(B, Hq, S, D, generator=g).to(dev, torch.bfloat16)
+    return q, k, v, do
+
+
+def _run(q, k, v, do, doc, **kw):
+    qr, kr, vr = (t.detach().requires_grad_(True) for t in (q, k, v))
+    out = doc_attention(qr, kr, vr, doc, **kw)
+    out.backward(do)
+    return out, qr.grad, kr.grad, vr.grad
+
+
+def _check(q, k, v, do, doc, what, **kw):
+    out, dq, dk, dv = _run(q, k, v, do, doc, **kw)
+    ref = OA.attention(q, k, v, doc.cpu(), do)
+    _close(out, ref["out"], f"{what} out")
+    _close(dq, ref["dq"], f"{what} dq")
+    _close(dk, ref["dk"], f"{what} dk")
+    _close(dv, ref["dv"], f"{what} dv")
+
+
+def test_reference_flex_test_case(dev) -> None:
+    """tests/test_attention.py:58-73 of the reference: fp32 q/k/v [1,2,64,16]."""
+    torch.manual_seed(0)
+    q = torch.randn(1, 2, 64, 16, device=dev)
+    k = torch.randn(1, 2, 64, 16, device=dev)
+    v = torch.randn(1, 2, 64, 16, device=dev)
+    doc_ids = torch.tensor([[0] * 20 + [1] * 44], device=dev)
+    mask = build_doc_block_mask(doc_ids, n_heads=2)
+    out = flex_attention(q, k, v, block_mask=mask)
+    assert out.dtype == torch.float32 and out.shape == q.shape
+    ref = OA.attention(q, k, v, doc_ids.cpu(), semantics="eager")["out"]
+    torch.testing.assert_close(out.cpu().double(), ref, atol=2e-2, rtol=2e-2)
+
+
+@pytest.mark.parametrize(
+    "B,Hq,Hkv,S,D,docs",
+    [
+        (1, 2, 2, 64, 16, [20, 44]),
+        (1, 4, 2, 256, 32, [60, 50, 100, 46]),  # cfg1 shape
+        (2, 4, 1, 300, 64, [100, 150, -50]),  # -n: n pad tokens (doc -1)
+        (1, 12, 4, 2048, 64, "cfg2"),  # cfg2 shape, heavy-tail pack
+        (1, 8, 8, 1000, 128, [1000]),  # one dense doc, S not a tile multiple
+        (1, 6, 2, 200, 128, [1] * 50 + [150]),  # single-token documents
+        (3, 4, 4, 130, 100, [64, 66]),  # head dim not a multiple of 16
+    ],
+)
+def test_attention_matches_oracle(B, Hq, Hkv, S, D, docs, dev) -> None:
+    if docs == "cfg2":
+        packs = W.cfg2_steps(1)[0][:B]
+    else:
+        pad = sum(-d for d in docs if d < 0)
+        packs = [[d for d in docs if d > 0]] * B
+        assert sum(packs[0]) + pad == S
+    doc = W.doc_ids_from_lengths(packs, S).to(dev)
+    q, k, v, do = _inputs(B, Hq, Hkv, S, D, dev, seed=S + D)
+    _check(q, k, v, do, doc, f"B{B} Hq{Hq} Hkv{Hkv} S{S} D{D}")
+
+
+def test_attention_contiguous_layout_and_scale(dev) -> None:
+    q, k, v, do = _inputs(1, 4, 2, 192, 64, dev, model_layout=False)
+    doc = W.doc_ids_from_lengths([[70, 122]], 192).to(dev)
+    out, dq, dk, dv = _run(q, k, v, do, doc, scale=0.3)
+    ref = OA.attention(q, k, v, doc.cpu(), do, scale=0.3)
+    _close(out, ref["out"], "out")
+    _close(dq, ref["dq"], "dq")
+    _close(dk, ref["dk"], "dk")
+    _close(dv, ref["dv"], "dv")
+
+
+def test_attention_noncontiguous_documents(dev) -> None:
+    """A document id may appear in several runs: the mask compares ids, not ranges."""
+    S = 160
+    ids = torch.tensor([i % 3 for i in range(S)], device=dev)[None]
+    q, k, v, do = _inputs(1, 2, 1, S, 32, dev, seed=7)
+    _check(q, k, v, do, ids, "alternating docs")
+
+
+def test_attention_forward_dispatch_and_eager_rows(dev) -> None:
+    packs = [[90, 100]]
+    S = 200  # 10 pad tokens
+    doc = W.doc_ids_from_lengths(packs, S).to(dev)
+    q, k, v, _ = _inputs(1, 4, 2, S, 64, dev, seed=3)
+    bm = build_doc_block_mask(doc, 4)
+    out = attention_forward(q, k, v, doc, block_mask=bm)
+    eager = OA.attention(q, k, v, doc.cpu(), semantics="eager")["out"]
+    real = doc[0].cpu() >= 0
+    _close(out[:, :, real], eager[:, :, real], "real rows vs eager semantics")
+    with pytest.raises(ValueError):
+        attention_forward(q, k, v, doc, backend="nope")
+    with pytest.raises(RuntimeError):
+        attention_forward(q.cpu(), k.cpu(), v.cpu(), doc.cpu())
+
+
+def test_attention_deterministic(dev) -> None:
+    doc = W.doc_ids_from_lengths([[300, 212]], 512).to(dev)
+    q, k, v, do = _inputs(1, 8, 2, 512, 128, dev, seed=11)
+    a = _run(q, k, v, do, doc)
+    b = _run(q, k, v, do, doc)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("pack", [1, 0])
+def test_attention_cfg3_pack(pack, dev) -> None:
+    """cfg3 shape (S=8192, Hq=32, Hkv=8, D=128): all 8 packs run, one pack x one
+    KV group (4 query heads) is checked against the oracle in full (fp32 oracle
+    arithmetic for speed; its formulas are pinned in float64 on the CPU)."""
+    packs = W.cfg3_packs()
+    S, Hq, Hkv, D = 8192, 32, 8, 128
+    doc = W.doc_ids_from_lengths(packs, S).to(dev)
+    q, k, v, do = _inputs(8, Hq, Hkv, S, D, dev, seed=3)
+    out, dq, dk, dv = _run(q, k, v, do, doc)
+    g = 5  # KV head 5 -> query heads 20..23
+    hs = slice(4 * g, 4 * g + 4)
+    sl = slice(pack, pack + 1)
+    ref = OA.attention(q[sl, hs], k[sl, g : g + 1], v[sl, g : g + 1], doc[sl].cpu(),
+                       do[sl, hs], dtype=torch.float32)
+    _close(out[sl, hs], ref["out"], "out")
+    _close(dq[sl, hs], ref["dq"], "dq")
+    _close(dk[sl, g : g + 1], ref["dk"], "dk")
+    _close(dv[sl, g : g + 1], ref["dv"], "dv")
+    assert torch.isfinite(out.float()).all() and torch.isfinite(dq.float()).all()

@@ -83,3 +83,30 @@ def test_block_tables_random_layouts(seed, dev) -> None:
 def test_build_doc_block_mask_rejects_batch(dev) -> None:
     with pytest.raises(ValueError):
         build_doc_block_mask(torch.zeros(2, 64, dtype=torch.long, device=dev), 2)
+
+
+@pytest.mark.parametrize("q_tile,kv_tile,by_kv", [(128, 64, 0), (32, 128, 1), (64, 64, 0)])
+def test_attention_plans_match_oracle(q_tile, kv_tile, by_kv, dev) -> None:
+    """pb_attn_plan lists == the closed-form tile classes, ascending, FULL bit set."""
+    from packbalance_amd import _native as N
+
+    packs = W.cfg3_packs()[:3] + [[5000, 3000, 192]]
+    s = 8192
+    doc = W.doc_ids_from_lengths(packs, s).to(dev)
+    b = doc.shape[0]
+    nq, nk = -(-s // q_tile), -(-s // kv_tile)
+    rows, cols = (nk, nq) if by_kv else (nq, nk)
+    counts = torch.empty((b, rows), dtype=torch.int32, device=dev)
+    lists = torch.full((b, rows, cols), -7, dtype=torch.int32, device=dev)
+    ws = torch.empty(b * nq * nk, dtype=torch.uint8, device=dev)
+    N.call("pb_attn_plan", doc.data_ptr(), doc.stride(0), b, s, q_tile, kv_tile, by_kv,
+           counts.data_ptr(), lists.data_ptr(), ws.data_ptr(), N.stream_ptr(doc))
+    counts, lists = counts.cpu().numpy(), lists.cpu().numpy()
+    for i in range(b):
+        cls = OB.classify_closed(doc[i].cpu().numpy(), q_tile, kv_tile)
+        if by_kv:
+            cls = cls.T
+        for r in range(rows):
+            want = [(c << 1) | int(cls[r, c] == OB.FULL) for c in range(cols) if cls[r, c]]
+            assert counts[i, r] == len(want), (i, r)
+            assert lists[i, r, : len(want)].tolist() == want, (i, r)
