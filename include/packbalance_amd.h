@@ -167,6 +167,48 @@ int pb_attn_bwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v, const pb_b
                 const int32_t *kv_plan_lists, int64_t b, int64_t hq, int64_t hkv, int64_t s,
                 int64_t d, float scale, int dtype, void *stream);
 
+/* ---- Fused LM-head cross-entropy ----------------------------------------
+ * Replaces packbalance/kernels/fused_ce.py:143-217 (_FusedLinearCE /
+ * linear_cross_entropy).  x [n, d] and w [v, d] are bf16 with 16-byte aligned
+ * rows, d % 8 == 0 (row strides ldx, ldw).  The logits x w^T are computed by
+ * bf16 MFMA tiles with fp32 accumulation and reduced in registers; they are
+ * never written.  Per row: lse (fp32, natural log) and
+ *   loss_rows[r] = lse - logit_t + z*lse^2   (0 if t == ignore_index,
+ *                                              NaN if t is outside [0, v)),
+ * loss_sum[0] = fixed-order fp32 sum of loss_rows.
+ * workspace: pb_lmhead_ce_workspace_bytes(n, v) bytes.                     */
+int64_t pb_lmhead_ce_workspace_bytes(int64_t n, int64_t v);
+int pb_lmhead_ce_fwd(const void *x, int64_t ldx, const void *w, int64_t ldw, int64_t n,
+                     int64_t v, int64_t d, const int64_t *targets, int64_t ignore_index,
+                     float z_loss_coeff, float *loss_rows, float *lse, float *loss_sum,
+                     void *workspace, void *stream);
+
+/* Backward of pb_lmhead_ce_fwd (fused_ce.py:176-202), vocab chunk by vocab
+ * chunk (vchunk rows of w, a multiple of 8):
+ *   dL = (softmax*(1 + 2z*lse) - onehot) * grad_out   (bf16, one chunk)
+ *   dx = sum over chunks dL w_chunk   (fp32 in dx_acc [n, d], row stride d;
+ *                                      written to dx in dx_dtype at the end)
+ *   dw[chunk] = dL^T x                (written in dw_dtype)
+ * xt = x^T [d, >= n] and wt = w^T [d, >= v] (bf16, e.g. from pb_pack_bf16);
+ * dl [n, ldl >= vchunk] and dlt [vchunk, ldlt >= n] are bf16 workspaces.
+ * grad_out is a device pointer to one fp32 (no host synchronisation).       */
+int pb_lmhead_ce_bwd(const void *x, int64_t ldx, const void *w, int64_t ldw, const void *xt,
+                     int64_t ldxt, const void *wt, int64_t ldwt, int64_t n, int64_t v,
+                     int64_t d, const int64_t *targets, int64_t ignore_index,
+                     float z_loss_coeff, const float *lse, const float *grad_out,
+                     int64_t vchunk, void *dl, int64_t ldl, void *dlt, int64_t ldlt,
+                     float *dx_acc, void *dx, int dx_dtype, int64_t lddx, void *dw,
+                     int dw_dtype, int64_t lddw, void *stream);
+
+/* Layout helper of the CE path: dst (bf16) <- src (any float dtype), cast
+ * and, if transpose, transposed; dst is [dst_rows, dst_cols] with row stride
+ * dst_ld, and every dst element outside the copied [rows, cols] (or
+ * [cols, rows]) block is written as zero (padding).  No reference
+ * counterpart: it feeds the K-contiguous operands the MFMA tiles read.      */
+int pb_pack_bf16(const void *src, int src_dtype, int64_t src_ld, int64_t rows, int64_t cols,
+                 void *dst, int64_t dst_ld, int64_t dst_rows, int64_t dst_cols, int transpose,
+                 void *stream);
+
 #ifdef __cplusplus
 }
 #endif

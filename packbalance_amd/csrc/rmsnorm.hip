@@ -405,7 +405,7 @@ extern "C" int pb_rmsnorm_bwd(const void *dy, int64_t dy_row_stride, const void 
   hipStream_t st = as_stream(stream);
   if (rows == 0) {
     // dw of an empty batch is zero.
-    hipMemsetAsync(dw, 0, (size_t)n * dtype_bytes(w_dtype), st);
+    (void)hipMemsetAsync(dw, 0, (size_t)n * dtype_bytes(w_dtype), st);
     return launch_status("pb_rmsnorm_bwd(empty)");
   }
   PB_CHECK_ARG(workspace != nullptr, "pb_rmsnorm_bwd: workspace is required");

@@ -1,8 +1,24 @@
-"""Cross-entropy kernels on gfx950: the row CE over materialised logits.
+"""Fused linear cross-entropy on gfx950: the full logits are never materialised.
+
+``linear_cross_entropy(x, weight, targets, *, chunk_size=1024,
+ignore_index=-100, z_loss_coeff=0.0)`` has the contract of the reference
+``packbalance/kernels/fused_ce.py:205-217``: the SUM over rows with target !=
+ignore_index of ``lse(x W^T) - (x W^T)_t + z*lse^2``; backward returns ``dx`` in
+x's dtype and original shape and ``dw`` in W's dtype (fp32 accumulation).
+
+Forward: one MFMA GEMM kernel computes logits tiles in registers and keeps
+only per-token (max, sum-exp) partials and the target logit, then a combine
+kernel gives lse and the loss.  Backward streams the vocabulary in chunks of
+``VOCAB_CHUNK`` rows: a GEMM recomputes the chunk's logits and writes dlogits
+(bf16) directly, then two GEMMs accumulate dx and write the chunk's dW rows.
+Operands are bf16 with fp32 accumulation (fp32 inputs are rounded to bf16,
+as the reference's autocast GEMM does).  ``chunk_size`` (token rows per
+chunk in the reference) is accepted and validated; memory is bounded by the
+vocab chunk instead.
 
 ``ce_rows`` is the contract of the reference's ``_ce_launch`` / ``_ce_kernel``
-(``packbalance/kernels/fused_ce.py:31-118``): per-row loss (and optionally
-dlogits) over a ``[M, V]`` logits block with any strides.
+(``fused_ce.py:31-118``): per-row loss (and optionally dlogits) over a
+materialised ``[M, V]`` logits block with any strides.
 """
 
 from __future__ import annotations
@@ -49,3 +65,114 @@ def ce_rows(logits: torch.Tensor, targets: torch.Tensor, *, write_dlogits: bool,
         m, v, int(ignore_index), float(z_loss_coeff), N.stream_ptr(logits),
     )
     return loss, lse, dl
+
+
+VOCAB_CHUNK = 8192
+
+
+def _round8(n: int) -> int:
+    return (n + 7) // 8 * 8
+
+
+def _bf16_rows(t: torch.Tensor) -> torch.Tensor:
+    """t [rows, k] as bf16 rows with 16-byte aligned starts and k padded to a multiple of 8."""
+    rows, k = t.shape
+    if (t.dtype == torch.bfloat16 and t.stride(1) == 1 and k % 8 == 0 and t.stride(0) % 8 == 0
+            and t.data_ptr() % 16 == 0):
+        return t
+    k8 = _round8(k)
+    out = torch.empty((rows, k8), dtype=torch.bfloat16, device=t.device)
+    src = t if t.stride(1) == 1 else t.contiguous()
+    N.call("pb_pack_bf16", src.data_ptr(), N.dtype_code(src), src.stride(0), rows, k,
+           out.data_ptr(), k8, rows, k8, 0, N.stream_ptr(t))
+    return out
+
+
+def _transpose_bf16(t: torch.Tensor) -> torch.Tensor:
+    """t [rows, k] bf16 -> [k, round8(rows)] bf16, zero-padded."""
+    rows, k = t.shape
+    r8 = _round8(rows)
+    out = torch.empty((k, r8), dtype=torch.bfloat16, device=t.device)
+    N.call("pb_pack_bf16", t.data_ptr(), N.PB_BF16, t.stride(0), rows, k, out.data_ptr(), r8,
+           k, r8, 1, N.stream_ptr(t))
+    return out
+
+
+class _FusedLinearCE(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, weight, targets, chunk_size, ignore_index, z_loss_coeff):
+        x2d = x.reshape(-1, x.shape[-1])
+        t1d = targets.reshape(-1)
+        if x2d.shape[0] != t1d.shape[0]:
+            raise ValueError(f"x has {x2d.shape[0]} rows but targets has {t1d.shape[0]}")
+        if weight.dim() != 2 or weight.shape[1] != x2d.shape[1]:
+            raise ValueError(f"weight {tuple(weight.shape)} does not match x features {x2d.shape[1]}")
+        n, d = x2d.shape
+        v = weight.shape[0]
+        dev = x.device
+        t = t1d.to(torch.int64).contiguous()
+        total = torch.zeros((), dtype=torch.float32, device=dev)
+        ctx.x_shape, ctx.x_dtype, ctx.w_dtype, ctx.d = x.shape, x.dtype, weight.dtype, d
+        ctx.ignore_index, ctx.z = int(ignore_index), float(z_loss_coeff)
+        if n == 0:
+            ctx.save_for_backward(x2d, weight, t, total)
+            ctx.empty = True
+            return total
+        ctx.empty = False
+        xb = _bf16_rows(x2d)
+        wb = _bf16_rows(weight)
+        lse = torch.empty(n, dtype=torch.float32, device=dev)
+        rows = torch.empty(n, dtype=torch.float32, device=dev)
+        ws = torch.empty(max(1, N.lib().pb_lmhead_ce_workspace_bytes(n, v) // 4),
+                         dtype=torch.float32, device=dev)
+        N.call("pb_lmhead_ce_fwd", xb.data_ptr(), xb.stride(0), wb.data_ptr(), wb.stride(0),
+               n, v, xb.shape[1], t.data_ptr(), ctx.ignore_index, ctx.z, rows.data_ptr(),
+               lse.data_ptr(), total.data_ptr(), ws.data_ptr(), N.stream_ptr(x))
+        ctx.save_for_backward(xb, wb, t, lse)
+        return total
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        xb, wb, t, lse = ctx.saved_tensors
+        if ctx.empty:
+            dw = torch.zeros(wb.shape, dtype=ctx.w_dtype, device=wb.device)
+            return (torch.zeros(ctx.x_shape, dtype=ctx.x_dtype, device=xb.device), dw,
+                    None, None, None, None)
+        n, d8 = xb.shape
+        v = wb.shape[0]
+        dev = xb.device
+        xt = _transpose_bf16(xb)  # [d8, n8]
+        wt = _transpose_bf16(wb)  # [d8, v8]
+        vchunk = min(VOCAB_CHUNK, _round8(v))
+        dl = torch.empty((n, vchunk), dtype=torch.bfloat16, device=dev)
+        dlt = torch.empty((vchunk, xt.shape[1]), dtype=torch.bfloat16, device=dev)
+        dx_acc = torch.empty((n, d8), dtype=torch.float32, device=dev)
+        dx = torch.empty((n, d8), dtype=ctx.x_dtype, device=dev)
+        dw = torch.empty((v, d8), dtype=ctx.w_dtype, device=dev)
+        go = grad_output.detach().to(torch.float32).reshape(1).contiguous()
+        N.call("pb_lmhead_ce_bwd", xb.data_ptr(), xb.stride(0), wb.data_ptr(), wb.stride(0),
+               xt.data_ptr(), xt.stride(0), wt.data_ptr(), wt.stride(0), n, v, d8,
+               t.data_ptr(), ctx.ignore_index, ctx.z, lse.data_ptr(), go.data_ptr(), vchunk,
+               dl.data_ptr(), dl.stride(0), dlt.data_ptr(), dlt.stride(0), dx_acc.data_ptr(),
+               dx.data_ptr(), N.dtype_code(dx), dx.stride(0), dw.data_ptr(), N.dtype_code(dw),
+               dw.stride(0), N.stream_ptr(xb))
+        d = ctx.d
+        if d8 != d:
+            dx, dw = dx[:, :d], dw[:, :d]
+        return dx.reshape(ctx.x_shape), dw, None, None, None, None
+
+
+def linear_cross_entropy(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    targets: torch.Tensor,
+    *,
+    chunk_size: int = 1024,
+    ignore_index: int = -100,
+    z_loss_coeff: float = 0.0,
+) -> torch.Tensor:
+    """Return the summed CE loss for ``x @ weight.T`` without full logits (gfx950 kernels)."""
+    N.require_device(x, weight, targets, op="linear_cross_entropy")
+    if int(chunk_size) <= 0:
+        raise ValueError("chunk_size must be positive")
+    return _FusedLinearCE.apply(x, weight, targets, int(chunk_size), ignore_index, z_loss_coeff)

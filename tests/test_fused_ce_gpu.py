@@ -1,0 +1,162 @@
+"""GPU parity: fused LM-head cross-entropy (loss, dx, dW) vs the oracle.
+
+The oracle is float64 CE over the bf16-rounded x and W (the kernel's operands;
+the reference's autocast GEMM rounds them the same way).  Tolerances: loss
+within 1e-4 relative (the CE bar); dx / dW (computed from bf16 dlogits)
+within 2e-2 (the reference GPU test's tolerance, tests/test_kernels.py:84-104)
+and within 1e-2 in relative Frobenius norm.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import kernels as OK
+from packbalance_amd.kernels.fused_ce import linear_cross_entropy
+
+pytestmark = pytest.mark.gpu
+
+
+def _rel_fro(got: torch.Tensor, want: torch.Tensor) -> float:
+    g, w = got.detach().double().cpu(), want.double().cpu()
+    return float((g - w).norm() / w.norm().clamp_min(1e-30))
+
+
+def _case(n_shape, v, d, xdtype, wdtype, dev, *, seed=0, wstd=1.0, ignore_every=0, ignore_p=0.0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(*n_shape, d, generator=g).to(dev, xdtype)
+    w = (torch.randn(v, d, generator=g) * wstd).to(dev, wdtype)
+    t = torch.randint(0, v, n_shape, generator=g)
+    if ignore_every:
+        t.view(-1)[::ignore_every] = -100
+    if ignore_p:
+        t[torch.rand(n_shape, generator=g) < ignore_p] = -100
+    return x, w, t.to(dev)
+
+
+def _check(x, w, t, z, what, *, chunk=1024):
+    xr = x.detach().requires_grad_(True)
+    wr = w.detach().requires_grad_(True)
+    loss = linear_cross_entropy(xr, wr, t, chunk_size=chunk, z_loss_coeff=z)
+    loss.backward()
+    l_ref, dx_ref, dw_ref = OK.linear_ce(x.to(torch.bfloat16), w.to(torch.bfloat16), t,
+                                         z_loss_coeff=z)
+    assert loss.dtype == torch.float32 and loss.dim() == 0
+    torch.testing.assert_close(loss.double().cpu(), l_ref, rtol=1e-4, atol=1e-4,
+                               msg=lambda m: f"{what} loss: {m}")
+    assert xr.grad.shape == x.shape and xr.grad.dtype == x.dtype
+    assert wr.grad.shape == w.shape and wr.grad.dtype == w.dtype
+    torch.testing.assert_close(xr.grad.double().cpu(), dx_ref, rtol=2e-2, atol=2e-2,
+                               msg=lambda m: f"{what} dx: {m}")
+    torch.testing.assert_close(wr.grad.double().cpu(), dw_ref, rtol=2e-2, atol=2e-2,
+                               msg=lambda m: f"{what} dw: {m}")
+    assert _rel_fro(xr.grad, dx_ref) < 1e-2, what
+    assert _rel_fro(wr.grad, dw_ref) < 1e-2, what
+
+
+def test_reference_gpu_case(dev) -> None:
+    """tests/test_kernels.py:84-104: x [2,32,32] fp32, w [128,32], every 5th ignored, z=0.01."""
+    torch.manual_seed(0)
+    x = torch.randn(2, 32, 32, device=dev)
+    w = torch.randn(128, 32, device=dev)
+    t = torch.randint(0, 128, (2, 32), device=dev)
+    t[:, ::5] = -100
+    _check(x, w, t, 0.01, "reference case", chunk=16)
+
+
+@pytest.mark.parametrize(
+    "shape,v,d,xdt,wdt,z",
+    [
+        ((37,), 64, 32, torch.float32, torch.float32, 0.0),
+        ((37,), 64, 32, torch.float32, torch.float32, 0.01),
+        ((300,), 1000, 96, torch.bfloat16, torch.bfloat16, 0.0),
+        ((129,), 8200, 64, torch.bfloat16, torch.bfloat16, 0.0),  # 2 vocab chunks, ragged
+        ((4, 50), 517, 40, torch.float32, torch.float32, 0.0),  # d % 8 != 0, v odd
+        ((2048,), 32000, 768, torch.float32, torch.float32, 0.0),  # cfg2 dtype flow
+    ],
+)
+def test_fused_ce_matches_oracle(shape, v, d, xdt, wdt, z, dev) -> None:
+    x, w, t = _case(shape, v, d, xdt, wdt, dev, seed=v + d, wstd=0.05 if d >= 256 else 1.0,
+                    ignore_every=7)
+    _check(x, w, t, z, f"{shape}x{v}x{d}")
+
+
+def test_fused_ce_all_ignored_and_empty(dev) -> None:
+    x = torch.randn(9, 16, device=dev, requires_grad=True)
+    w = torch.randn(24, 16, device=dev, requires_grad=True)
+    t = torch.full((9,), -100, device=dev)
+    loss = linear_cross_entropy(x, w, t)
+    loss.backward()
+    assert float(loss) == 0.0
+    assert float(x.grad.abs().sum()) == 0.0 and float(w.grad.abs().sum()) == 0.0
+    x0 = torch.randn(0, 16, device=dev, requires_grad=True)
+    l0 = linear_cross_entropy(x0, w, torch.zeros(0, dtype=torch.long, device=dev))
+    l0.backward()
+    assert float(l0) == 0.0 and x0.grad.shape == (0, 16)
+
+
+def test_fused_ce_errors(dev) -> None:
+    with pytest.raises(ValueError):
+        linear_cross_entropy(torch.randn(4, 8, device=dev), torch.randn(5, 8, device=dev),
+                             torch.zeros(3, dtype=torch.long, device=dev))
+    with pytest.raises(RuntimeError):
+        linear_cross_entropy(torch.randn(4, 8), torch.randn(5, 8), torch.zeros(4, dtype=torch.long))
+
+
+def test_fused_ce_grad_output_scaling(dev) -> None:
+    x, w, t = _case((64,), 300, 32, torch.bfloat16, torch.bfloat16, dev, seed=5)
+    xr = x.detach().requires_grad_(True)
+    wr = w.detach().requires_grad_(True)
+    (linear_cross_entropy(xr, wr, t) * 0.25).backward()
+    _, dx_ref, dw_ref = OK.linear_ce(x, w, t)
+    torch.testing.assert_close(xr.grad.double().cpu(), dx_ref * 0.25, rtol=2e-2, atol=2e-2)
+    torch.testing.assert_close(wr.grad.double().cpu(), dw_ref * 0.25, rtol=2e-2, atol=2e-2)
+
+
+def test_fused_ce_cfg4_full_size(dev) -> None:
+    """cfg4: x [16384, 4096] bf16 ~N(0,1), W [128256, 4096] bf16 ~N(0, 0.02), 1% ignored.
+
+    Every output against a torch fp32 evaluation on the device (row chunks of
+    logits, never the whole [N, V] block at once); 32 sampled rows of loss and
+    dx against the float64 oracle.
+    """
+    N, V, D = 16384, 128256, 4096
+    torch.manual_seed(0)
+    x = torch.randn(N, D, device=dev, dtype=torch.bfloat16)
+    w = (torch.randn(V, D, device=dev) * 0.02).to(torch.bfloat16)
+    t = torch.randint(0, V, (N,), device=dev)
+    t[torch.rand(N, device=dev) < 0.01] = -100
+    xr = x.detach().requires_grad_(True)
+    wr = w.detach().requires_grad_(True)
+    loss = linear_cross_entropy(xr, wr, t)
+    loss.backward()
+
+    wf = w.float()
+    ref_loss = torch.zeros((), device=dev, dtype=torch.float64)
+    dx_ref = torch.empty(N, D, device=dev)
+    dw_ref = torch.zeros(V, D, device=dev)
+    for r in range(0, N, 2048):
+        xs = x[r : r + 2048].float()
+        ts = t[r : r + 2048]
+        logits = xs @ wf.t()
+        lse = torch.logsumexp(logits, dim=-1)
+        valid = ts != -100
+        safe = torch.where(valid, ts, torch.zeros_like(ts))
+        tl = logits.gather(1, safe[:, None])[:, 0]
+        ref_loss += torch.where(valid, lse - tl, torch.zeros_like(lse)).double().sum()
+        p = torch.softmax(logits, dim=-1)
+        p[torch.arange(p.shape[0], device=dev), safe] -= 1.0
+        p[~valid] = 0.0
+        dx_ref[r : r + 2048] = p @ wf
+        dw_ref += p.t() @ xs
+        del logits, p
+    torch.testing.assert_close(loss.double(), ref_loss, rtol=1e-4, atol=1e-4)
+    torch.testing.assert_close(xr.grad.float(), dx_ref, rtol=2e-2, atol=2e-2)
+    torch.testing.assert_close(wr.grad.float(), dw_ref, rtol=2e-2, atol=2e-2)
+    assert _rel_fro(xr.grad.float(), dx_ref) < 1e-2
+    assert _rel_fro(wr.grad.float(), dw_ref) < 1e-2
+    rows = torch.randperm(N, generator=torch.Generator().manual_seed(1))[:32].to(dev)
+    l_rows, dx_rows, _ = OK.linear_ce(x[rows], w, t[rows])
+    torch.testing.assert_close(dx_rows, xr.grad[rows].double().cpu(), rtol=2e-2, atol=2e-2)
+    del l_rows
