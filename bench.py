@@ -1,0 +1,454 @@
+#!/usr/bin/env python
+"""Benchmark of PackBalance's training hot path on one MI355X.
+
+Headline (``value``): useful tokens/s of the 100M Llama packed-2048 training
+step (4 packs of 2048 tokens per step, heavy-tail lognormal documents packed
+best-fit-decreasing, bf16 autocast with fp32 master weights, clip + fused
+AdamW) -- the semantics of the reference's ``profiling/bench_train.py:54-163``:
+useful tok/s = sum of pack tokens / sum of timed step seconds.
+
+Kernel figures (HIP events around each C-ABI launch, on the stream the kernel
+runs on):
+  attention  cfg3 masked GQA attention fwd+bwd, 12*D*Hq*P FLOPs (P = allowed pairs)
+  lmhead_ce  cfg4 fused LM-head CE fwd+bwd, 6*N*V*D FLOPs
+  ce_rows    one cfg4 vocab chunk [16384 x 8192] bf16 through the row CE kernel
+  rmsnorm / swiglu   cfg5 fwd and bwd, algorithmic bytes moved
+The ``roofline`` object is the attention forward kernel at cfg3 (MFMA-bound).
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--skip-cpu] [--skip-kernels]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_model_name() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+# ---------------------------------------------------------------- timing
+def events_ms(launch, iters: int, flush=None) -> float:
+    """Mean duration (ms) of `launch()` over `iters` calls, each bracketed by events."""
+    import torch
+
+    total = 0.0
+    for _ in range(iters):
+        if flush is not None:
+            flush()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        launch()
+        e.record()
+        e.synchronize()
+        total += s.elapsed_time(e)
+    return total / iters
+
+
+def make_flush(dev):
+    import torch
+
+    buf = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev)
+
+    def flush():
+        buf.fill_(1.0)  # evicts the 256 MB last-level cache between HBM-bound launches
+
+    return flush
+
+
+# ---------------------------------------------------------------- cfg2 train step
+def train_step_bench(steps: int, warmup: int, dev):
+    import numpy as np
+    import torch
+
+    from packbalance_amd.data import workloads as W
+    from packbalance_amd.model.attention import build_doc_block_mask
+    from packbalance_amd.model.llama import LlamaForCausalLM, cfg2_model, count_parameters
+
+    cfg = cfg2_model()
+    torch.manual_seed(0)
+    model = LlamaForCausalLM(cfg).to(dev)
+    model.train()
+    opt = torch.optim.AdamW(model.parameters(), lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1,
+                            fused=True)
+    plan = W.cfg2_steps(warmup + steps)
+    rng = np.random.default_rng(0)
+    batches = [[W.pack_tensors([p], 2048, cfg.vocab_size, rng).to(dev) for p in st] for st in plan]
+
+    def run(step_batches):
+        opt.zero_grad(set_to_none=True)
+        step_tokens = sum(b.useful_tokens for b in step_batches)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            for b in step_batches:
+                bm = build_doc_block_mask(b.doc_ids, cfg.n_heads)
+                loss = model(b.input_ids, b.labels, b.position_ids, b.doc_ids, block_mask=bm)
+                (loss / step_tokens).backward()
+        torch.nn.utils.clip_grad_norm_(model.parameters(), 1.0)
+        opt.step()
+
+    for i in range(warmup):
+        run(batches[i])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(warmup, warmup + steps):
+        run(batches[i])
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    useful = sum(b.useful_tokens for st in batches[warmup:] for b in st)
+    from oracle.model import step_flops
+
+    flops = sum(step_flops(cfg, [b.doc_lengths[0] for b in st]) for st in batches[warmup:])
+    res = {
+        "tok_s": useful / dt,
+        "ms_per_step": dt / steps * 1e3,
+        "useful_tokens": useful,
+        "params": count_parameters(model),
+        "model_tflops": flops / dt / 1e12,
+    }
+    return res, model, cfg, batches
+
+
+# ---------------------------------------------------------------- cpu baseline
+def cpu_baseline(model, cfg, batch) -> dict:
+    """The reference's CPU path restated (oracle/model.py), fp32, on this host's cores."""
+    import torch
+
+    from oracle import model as OM
+
+    params = OM.cpu_params(model)
+    b = batch.to("cpu")
+    t0 = time.perf_counter()
+    loss = OM.loss(params, cfg, b.input_ids, b.labels, b.position_ids, b.doc_ids)
+    loss.backward()
+    t_fb = time.perf_counter() - t0
+    opt = torch.optim.AdamW(list(params.values()), lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1)
+    t0 = time.perf_counter()
+    torch.nn.utils.clip_grad_norm_(list(params.values()), 1.0)
+    opt.step()
+    t_opt = time.perf_counter() - t0
+    step_s = 4 * t_fb + t_opt
+    tokens = 4 * b.useful_tokens
+    return {
+        "value": tokens / step_s,
+        "unit": "tok/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"one 2048-token pack fwd+bwd ({t_fb:.2f} s) plus one AdamW+clip step "
+                   f"({t_opt:.2f} s) of the eager fp32 CPU path on the 100M model, extrapolated "
+                   "to a 4-pack step; cpu " + cpu_model_name() +
+                   f", affinity {len(os.sched_getaffinity(0))} cores"),
+    }
+
+
+# ---------------------------------------------------------------- kernels
+def attention_kernels(dev, iters: int) -> dict:
+    import torch
+
+    from packbalance_amd import _native as N
+    from packbalance_amd.data import workloads as W
+    from packbalance_amd.model import attention as A
+
+    packs = W.cfg3_packs()
+    B, S, Hq, Hkv, D = 8, 8192, 32, 8, 128
+    doc = W.doc_ids_from_lengths(packs, S).to(dev)
+    torch.manual_seed(0)
+    q = torch.randn(B, S, Hq, D, device=dev, dtype=torch.bfloat16).transpose(1, 2)
+    k = torch.randn(B, S, Hkv, D, device=dev, dtype=torch.bfloat16).transpose(1, 2)
+    v = torch.randn(B, S, Hkv, D, device=dev, dtype=torch.bfloat16).transpose(1, 2)
+    do = torch.randn(B, S, Hq, D, device=dev, dtype=torch.bfloat16).transpose(1, 2)
+    plans = A._plans(doc, D, None)
+    out = torch.empty(B, S, Hq, D, device=dev, dtype=torch.bfloat16).transpose(1, 2)
+    lse = torch.empty(B, Hq, S, device=dev, dtype=torch.float32)
+    dq = torch.empty_like(out)
+    dk = torch.empty(B, S, Hkv, D, device=dev, dtype=torch.bfloat16).transpose(1, 2)
+    dv = torch.empty_like(dk)
+    delta = torch.empty_like(lse)
+    sc = 1.0 / D ** 0.5
+    st = N.stream_ptr(q)
+    pf, pq, pk = plans[A.FWD], plans[A.BWD_Q], plans[A.BWD_KV]
+
+    def fwd():
+        N.call("pb_attn_fwd", N.BHSD.of(q), N.BHSD.of(k), N.BHSD.of(v), N.BHSD.of(out),
+               lse.data_ptr(), doc.data_ptr(), doc.stride(0), pf.counts.data_ptr(),
+               pf.lists.data_ptr(), B, Hq, Hkv, S, D, sc, N.PB_BF16, st)
+
+    def bwd():
+        N.call("pb_attn_bwd", N.BHSD.of(q), N.BHSD.of(k), N.BHSD.of(v), N.BHSD.of(out),
+               N.BHSD.of(do), N.BHSD.of(dq), N.BHSD.of(dk), N.BHSD.of(dv), lse.data_ptr(),
+               delta.data_ptr(), doc.data_ptr(), doc.stride(0), pq.counts.data_ptr(),
+               pq.lists.data_ptr(), pk.counts.data_ptr(), pk.lists.data_ptr(), B, Hq, Hkv, S, D,
+               sc, N.PB_BF16, st)
+
+    fwd()
+    bwd()
+    torch.cuda.synchronize()
+    t_f = events_ms(fwd, iters)
+    t_b = events_ms(bwd, iters)
+    pairs = float(sum(L * (L + 1) // 2 for p in packs for L in p))
+    f_fwd = 4.0 * D * Hq * pairs
+    f_bwd = 8.0 * D * Hq * pairs
+    return {
+        "workload": "cfg3: 8 packs x 8192, Hq 32, Hkv 8, D 128, bf16, pack 0 dense",
+        "allowed_pairs_per_head": pairs,
+        "fwd_ms": t_f, "bwd_ms": t_b,
+        "fwd_tflops": f_fwd / t_f / 1e9, "bwd_tflops": f_bwd / t_b / 1e9,
+        "fwd_bwd_tflops": (f_fwd + f_bwd) / (t_f + t_b) / 1e9,
+        "frac_bf16_peak": (f_fwd + f_bwd) / (t_f + t_b) / 1e9 / PEAK_BF16_TFLOPS,
+        "fwd_flops_per_launch": f_fwd,
+    }
+
+
+def lmhead_ce_kernels(dev, iters: int) -> dict:
+    import torch
+
+    from packbalance_amd.kernels.fused_ce import linear_cross_entropy
+
+    Nt, V, D = 16384, 128256, 4096
+    torch.manual_seed(0)
+    x = torch.randn(Nt, D, device=dev, dtype=torch.bfloat16).requires_grad_(True)
+    w = (torch.randn(V, D, device=dev) * 0.02).to(torch.bfloat16).requires_grad_(True)
+    t = torch.randint(0, V, (Nt,), device=dev)
+    t[torch.rand(Nt, device=dev) < 0.01] = -100
+    holder = {}
+
+    def fwd():
+        holder["loss"] = linear_cross_entropy(x, w, t)
+
+    def bwd():
+        holder["loss"].backward()
+
+    fwd()
+    bwd()
+    torch.cuda.synchronize()
+    tf = tb = 0.0
+    for _ in range(iters):
+        x.grad = None
+        w.grad = None
+        tf += events_ms(fwd, 1)
+        tb += events_ms(bwd, 1)
+    tf /= iters
+    tb /= iters
+    flops = 6.0 * Nt * V * D
+    return {
+        "workload": "cfg4: x [16384, 4096] bf16, W [128256, 4096] bf16, 1% ignored, vocab chunk 8192",
+        "fwd_ms": tf, "bwd_ms": tb,
+        "tflops": flops / (tf + tb) / 1e9,
+        "frac_bf16_peak": flops / (tf + tb) / 1e9 / PEAK_BF16_TFLOPS,
+        "note": "fwd 2NVD + bwd 6NVD executed (logits recomputed once); 6NVD counted",
+    }
+
+
+def ce_rows_kernel(dev, iters: int, flush) -> dict:
+    import torch
+
+    from packbalance_amd import _native as N
+
+    m, v = 16384, 8192
+    torch.manual_seed(0)
+    logits = torch.randn(m, v, device=dev).to(torch.bfloat16)
+    t = torch.randint(0, v, (m,), device=dev)
+    loss = torch.empty(m, device=dev)
+    lse = torch.empty(m, device=dev)
+    dl = torch.empty_like(logits)
+    st = N.stream_ptr(logits)
+
+    def launch():
+        N.call("pb_ce_rows", logits.data_ptr(), v, 1, N.PB_BF16, t.data_ptr(), loss.data_ptr(),
+               lse.data_ptr(), dl.data_ptr(), m, v, -100, 0.0, st)
+
+    launch()
+    ms = events_ms(launch, iters, flush)
+    nbytes = 2 * m * v * 2 + m * 8 + 2 * m * 4
+    return {"workload": "one cfg4 vocab chunk: logits [16384, 8192] bf16 -> loss, lse, dlogits",
+            "ms": ms, "bytes": nbytes, "gbps": nbytes / ms / 1e6,
+            "frac_hbm_peak": nbytes / ms / 1e6 / PEAK_HBM_GBPS}
+
+
+def norm_act_kernels(dev, iters: int, flush) -> dict:
+    import torch
+
+    from packbalance_amd import _native as N
+
+    out = {}
+    R, H = 32768, 4096
+    torch.manual_seed(0)
+    x = torch.randn(R, H, device=dev, dtype=torch.bfloat16)
+    w = (torch.randn(H, device=dev) * 0.1 + 1.0).to(torch.bfloat16)
+    dy = torch.randn(R, H, device=dev, dtype=torch.bfloat16)
+    y = torch.empty_like(x)
+    dx = torch.empty_like(x)
+    dw = torch.empty_like(w)
+    rstd = torch.empty(R, device=dev)
+    ws = torch.empty(N.lib().pb_rmsnorm_bwd_workspace_bytes(R, H) // 4, device=dev)
+    st = N.stream_ptr(x)
+
+    def rf():
+        N.call("pb_rmsnorm_fwd", x.data_ptr(), H, N.PB_BF16, w.data_ptr(), N.PB_BF16, y.data_ptr(),
+               H, rstd.data_ptr(), R, H, 1e-5, st)
+
+    def rb():
+        N.call("pb_rmsnorm_bwd", dy.data_ptr(), H, x.data_ptr(), H, N.PB_BF16, w.data_ptr(),
+               N.PB_BF16, rstd.data_ptr(), dx.data_ptr(), H, dw.data_ptr(), ws.data_ptr(), R, H, st)
+
+    rf()
+    rb()
+    t_rf = events_ms(rf, iters, flush)
+    t_rb = events_ms(rb, iters, flush)
+    b_rf = 2 * R * H * 2 + H * 2 + R * 4
+    b_rb = 3 * R * H * 2 + R * 4 + 2 * H * 2
+    out["rmsnorm"] = {"workload": "cfg5: [32768, 4096] bf16, w bf16", "fwd_ms": t_rf,
+                      "bwd_ms": t_rb, "fwd_gbps": b_rf / t_rf / 1e6, "bwd_gbps": b_rb / t_rb / 1e6,
+                      "fwd_bwd_gbps": (b_rf + b_rb) / (t_rf + t_rb) / 1e6,
+                      "frac_hbm_peak": (b_rf + b_rb) / (t_rf + t_rb) / 1e6 / PEAK_HBM_GBPS}
+    del x, dy, y, dx
+    R, F = 32768, 14336
+    n = R * F
+    g = torch.randn(R, F, device=dev, dtype=torch.bfloat16)
+    u = torch.randn(R, F, device=dev, dtype=torch.bfloat16)
+    d = torch.randn(R, F, device=dev, dtype=torch.bfloat16)
+    o = torch.empty_like(g)
+    dg = torch.empty_like(g)
+    du = torch.empty_like(g)
+
+    def sf():
+        N.call("pb_swiglu_fwd", g.data_ptr(), u.data_ptr(), o.data_ptr(), n, N.PB_BF16, st)
+
+    def sb():
+        N.call("pb_swiglu_bwd", g.data_ptr(), u.data_ptr(), d.data_ptr(), dg.data_ptr(),
+               du.data_ptr(), n, N.PB_BF16, st)
+
+    sf()
+    sb()
+    t_sf = events_ms(sf, iters, flush)
+    t_sb = events_ms(sb, iters, flush)
+    out["swiglu"] = {"workload": "cfg5: gate/up [32768, 14336] bf16", "fwd_ms": t_sf,
+                     "bwd_ms": t_sb, "fwd_gbps": 3 * n * 2 / t_sf / 1e6,
+                     "bwd_gbps": 5 * n * 2 / t_sb / 1e6,
+                     "fwd_bwd_gbps": 8 * n * 2 / (t_sf + t_sb) / 1e6,
+                     "frac_hbm_peak": 8 * n * 2 / (t_sf + t_sb) / 1e6 / PEAK_HBM_GBPS}
+    return out
+
+
+# ---------------------------------------------------------------- main
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--kernel-iters", type=int, default=10)
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--skip-kernels", action="store_true")
+    ap.add_argument("--only", choices=["train", "attention", "lmhead_ce", "ce_rows", "norm_act"],
+                    default=None, help="run one part only (for profiling)")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(see the sharding design); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from packbalance_amd import _native as N
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    N.lib()
+    dev = torch.device("cuda:0")
+    torch.backends.cuda.matmul.allow_tf32 = True
+
+    if args.only and args.only != "train":
+        flush = make_flush(dev)
+        fn = {"attention": lambda: attention_kernels(dev, args.kernel_iters),
+              "lmhead_ce": lambda: lmhead_ce_kernels(dev, args.kernel_iters),
+              "ce_rows": lambda: ce_rows_kernel(dev, args.kernel_iters, flush),
+              "norm_act": lambda: norm_act_kernels(dev, args.kernel_iters, flush)}[args.only]
+        print(json.dumps({args.only: fn()}), flush=True)
+        return 0
+
+    log(f"train step: {args.warmup} warmup + {args.steps} timed steps")
+    train, model, cfg, batches = train_step_bench(args.steps, args.warmup, dev)
+    log(f"train: {train['tok_s']:.0f} tok/s, {train['ms_per_step']:.2f} ms/step")
+    if args.only == "train":
+        print(json.dumps({"train": train}), flush=True)
+        return 0
+
+    kernels = {}
+    roofline = None
+    if not args.skip_kernels:
+        flush = make_flush(dev)
+        log("kernels: attention (cfg3)")
+        kernels["attention"] = attention_kernels(dev, args.kernel_iters)
+        a = kernels["attention"]
+        roofline = {"bound": "mfma", "kernel": "attn_fwd_kernel<128> (cfg3)",
+                    "achieved": a["fwd_tflops"], "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                    "frac": a["fwd_tflops"] / PEAK_BF16_TFLOPS, "traffic": None}
+        log("kernels: fused LM-head CE (cfg4)")
+        kernels["lmhead_ce"] = lmhead_ce_kernels(dev, max(2, args.kernel_iters // 3))
+        log("kernels: row CE chunk")
+        kernels["ce_rows"] = ce_rows_kernel(dev, args.kernel_iters, flush)
+        log("kernels: RMSNorm / SwiGLU (cfg5)")
+        kernels.update(norm_act_kernels(dev, args.kernel_iters, flush))
+
+    base = None
+    if not args.skip_cpu:
+        log("cpu baseline (eager fp32 CPU path)")
+        base = cpu_baseline(model, cfg, batches[args.warmup][0])
+
+    line = {
+        "metric": "useful tok/s fwd+bwd (100M, 2048 packed); masked-attn TFLOP/s; CE GB/s",
+        "value": train["tok_s"],
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": train["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (lognormal docs, BFD packs, uniform token ids; random-init weights)",
+        "config": {
+            "workload": "cfg2: 100M Llama (12L, d768, Hq12/Hkv4, ffn2048, vocab32000, tied), "
+                        "4 packs x 2048 per step, bf16 autocast + fp32 master, AdamW",
+            "global_batch": 4,
+            "seq_len": 2048,
+            "parallelism": "single GPU",
+            "params": train["params"],
+            "model_tflops": train["model_tflops"],
+        },
+        "masked_attn_tflops": kernels.get("attention", {}).get("fwd_bwd_tflops"),
+        "ce_gbps": kernels.get("ce_rows", {}).get("gbps"),
+        "roofline": roofline,
+        "cpu_baseline": base,
+        "kernels": kernels,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
