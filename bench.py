@@ -79,41 +79,32 @@ def make_flush(dev):
 
 
 # ---------------------------------------------------------------- cfg2 train step
-def train_step_bench(steps: int, warmup: int, dev):
+def train_step_bench(steps: int, warmup: int, dev, use_graph: bool = True):
     import numpy as np
     import torch
 
     from packbalance_amd.data import workloads as W
-    from packbalance_amd.model.attention import build_doc_block_mask
-    from packbalance_amd.model.llama import LlamaForCausalLM, cfg2_model, count_parameters
+    from packbalance_amd.model.llama import cfg2_model, count_parameters
+    from packbalance_amd.model.step import TrainStep
 
     cfg = cfg2_model()
-    torch.manual_seed(0)
-    model = LlamaForCausalLM(cfg).to(dev)
-    model.train()
-    opt = torch.optim.AdamW(model.parameters(), lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1,
-                            fused=True)
+    ts = TrainStep(cfg, dev)
     plan = W.cfg2_steps(warmup + steps)
     rng = np.random.default_rng(0)
     batches = [[W.pack_tensors([p], 2048, cfg.vocab_size, rng).to(dev) for p in st] for st in plan]
-
-    def run(step_batches):
-        opt.zero_grad(set_to_none=True)
-        step_tokens = sum(b.useful_tokens for b in step_batches)
-        with torch.autocast("cuda", dtype=torch.bfloat16):
-            for b in step_batches:
-                bm = build_doc_block_mask(b.doc_ids, cfg.n_heads)
-                loss = model(b.input_ids, b.labels, b.position_ids, b.doc_ids, block_mask=bm)
-                (loss / step_tokens).backward()
-        torch.nn.utils.clip_grad_norm_(model.parameters(), 1.0)
-        opt.step()
-
+    tokens = [torch.tensor(float(sum(b.useful_tokens for b in st)), device=dev) for st in batches]
+    model = ts.model
+    if use_graph:
+        ts.capture(batches[0], tokens[0])
+        run = lambda i: ts.replay(batches[i], tokens[i])  # noqa: E731
+    else:
+        run = lambda i: ts.eager(batches[i])  # noqa: E731
     for i in range(warmup):
-        run(batches[i])
+        run(i)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(warmup, warmup + steps):
-        run(batches[i])
+        run(i)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     useful = sum(b.useful_tokens for st in batches[warmup:] for b in st)
@@ -126,6 +117,7 @@ def train_step_bench(steps: int, warmup: int, dev):
         "useful_tokens": useful,
         "params": count_parameters(model),
         "model_tflops": flops / dt / 1e12,
+        "hip_graph": use_graph,
     }
     return res, model, cfg, batches
 
@@ -178,13 +170,13 @@ def attention_kernels(dev, iters: int) -> dict:
     k = torch.randn(B, S, Hkv, D, device=dev, dtype=torch.bfloat16).transpose(1, 2)
     v = torch.randn(B, S, Hkv, D, device=dev, dtype=torch.bfloat16).transpose(1, 2)
     do = torch.randn(B, S, Hq, D, device=dev, dtype=torch.bfloat16).transpose(1, 2)
-    plans = A._plans(doc, D, None)
+    plans = A._plans(doc, Hq, Hkv, D, None)
     out = torch.empty(B, S, Hq, D, device=dev, dtype=torch.bfloat16).transpose(1, 2)
     lse = torch.empty(B, Hq, S, device=dev, dtype=torch.float32)
     dq = torch.empty_like(out)
     dk = torch.empty(B, S, Hkv, D, device=dev, dtype=torch.bfloat16).transpose(1, 2)
     dv = torch.empty_like(dk)
-    delta = torch.empty_like(lse)
+    ws = torch.empty(plans["workspace"], dtype=torch.uint8, device=dev)
     sc = 1.0 / D ** 0.5
     st = N.stream_ptr(q)
     pf, pq, pk = plans[A.FWD], plans[A.BWD_Q], plans[A.BWD_KV]
@@ -197,7 +189,7 @@ def attention_kernels(dev, iters: int) -> dict:
     def bwd():
         N.call("pb_attn_bwd", N.BHSD.of(q), N.BHSD.of(k), N.BHSD.of(v), N.BHSD.of(out),
                N.BHSD.of(do), N.BHSD.of(dq), N.BHSD.of(dk), N.BHSD.of(dv), lse.data_ptr(),
-               delta.data_ptr(), doc.data_ptr(), doc.stride(0), pq.counts.data_ptr(),
+               ws.data_ptr(), doc.data_ptr(), doc.stride(0), pq.counts.data_ptr(),
                pq.lists.data_ptr(), pk.counts.data_ptr(), pk.lists.data_ptr(), B, Hq, Hkv, S, D,
                sc, N.PB_BF16, st)
 
@@ -360,6 +352,8 @@ def main() -> int:
     ap.add_argument("--kernel-iters", type=int, default=10)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-kernels", action="store_true")
+    ap.add_argument("--eager", action="store_true",
+                    help="run the training step eagerly instead of as one captured HIP graph")
     ap.add_argument("--only", choices=["train", "attention", "lmhead_ce", "ce_rows", "norm_act"],
                     default=None, help="run one part only (for profiling)")
     args = ap.parse_args()
@@ -390,7 +384,8 @@ def main() -> int:
         return 0
 
     log(f"train step: {args.warmup} warmup + {args.steps} timed steps")
-    train, model, cfg, batches = train_step_bench(args.steps, args.warmup, dev)
+    train, model, cfg, batches = train_step_bench(args.steps, args.warmup, dev,
+                                                  use_graph=not args.eager)
     log(f"train: {train['tok_s']:.0f} tok/s, {train['ms_per_step']:.2f} ms/step")
     if args.only == "train":
         print(json.dumps({"train": train}), flush=True)
@@ -439,6 +434,7 @@ def main() -> int:
             "parallelism": "single GPU",
             "params": train["params"],
             "model_tflops": train["model_tflops"],
+            "hip_graph": train["hip_graph"],
         },
         "masked_attn_tflops": kernels.get("attention", {}).get("fwd_bwd_tflops"),
         "ce_gbps": kernels.get("ce_rows", {}).get("gbps"),

@@ -126,10 +126,12 @@ typedef struct pb_bhsd {
   int64_t stride_s;
 } pb_bhsd;
 
-/* Tile size of an attention kernel: kernel 0 = forward, 1 = dK/dV backward,
- * 2 = dQ backward; which 0 = query tile, 1 = key/value tile.  Plans passed to
- * pb_attn_fwd / pb_attn_bwd must be built with these sizes.                */
-int pb_attn_tile(int kernel, int64_t head_dim, int which);
+/* Launch configuration of the attention kernels for one problem shape (no
+ * reference counterpart).  out[0..7] = forward query tile, forward KV tile,
+ * dK/dV query tile, dK/dV KV tile, dQ query tile, dQ KV tile, pb_attn_bwd
+ * workspace bytes, dK/dV head-split flag.  Plans passed to pb_attn_fwd /
+ * pb_attn_bwd must be built with these tile sizes.                          */
+int pb_attn_config(int64_t b, int64_t hq, int64_t hkv, int64_t s, int64_t d, int64_t *out);
 
 /* Tile plan of a packed batch (no counterpart table in the reference; it is
  * the kernels' form of BlockMask.{kv,full_kv}_indices (by_kv = 0) or
@@ -146,9 +148,10 @@ int pb_attn_plan(const int64_t *doc_ids, int64_t doc_stride, int64_t b, int64_t 
  * (flex_attention(q, k, v, block_mask=doc mask, enable_gqa=Hq != Hkv)):
  *   out[b,h,i] = sum_j softmax_j(scale * q[b,h,i].k[b,h/G,j] | mask) v[b,h/G,j]
  * with mask(i, j) = doc[b,i] == doc[b,j] && i >= j, G = hq / hkv.
- * q/k/v/out are bf16 (dtype must be PB_BF16), head_dim d <= 128.
+ * q/k/v/out are bf16 (dtype must be PB_BF16), head_dim d <= 128, scale > 0.
  * lse (fp32 [b, hq, s]) receives log2(sum_j exp2(scale*log2(e)*q.k)) for the
- * backward.  plan = pb_attn_plan(by_kv = 0) with the kernel-0 tile sizes.   */
+ * backward.  plan = pb_attn_plan(by_kv = 0) with the forward tiles of
+ * pb_attn_config.                                                           */
 int pb_attn_fwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v, const pb_bhsd *out,
                 float *lse, const int64_t *doc_ids, int64_t doc_stride,
                 const int32_t *plan_counts, const int32_t *plan_lists, int64_t b,
@@ -156,12 +159,12 @@ int pb_attn_fwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v, const pb_b
                 void *stream);
 
 /* Replaces the FlexAttention backward (dQ, dK, dV; dK/dV summed over each
- * GQA group, as enable_gqa does).  delta_ws is an fp32 [b, hq, s] workspace.
- * kv_plan = pb_attn_plan(by_kv = 1) with the kernel-1 tile sizes,
- * q_plan  = pb_attn_plan(by_kv = 0) with the kernel-2 tile sizes.           */
+ * GQA group, as enable_gqa does).  workspace: out[6] bytes of pb_attn_config.
+ * kv_plan = pb_attn_plan(by_kv = 1) with the dK/dV tiles,
+ * q_plan  = pb_attn_plan(by_kv = 0) with the dQ tiles of pb_attn_config.     */
 int pb_attn_bwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v, const pb_bhsd *out,
                 const pb_bhsd *dout, const pb_bhsd *dq, const pb_bhsd *dk,
-                const pb_bhsd *dv, const float *lse, float *delta_ws,
+                const pb_bhsd *dv, const float *lse, void *workspace,
                 const int64_t *doc_ids, int64_t doc_stride, const int32_t *q_plan_counts,
                 const int32_t *q_plan_lists, const int32_t *kv_plan_counts,
                 const int32_t *kv_plan_lists, int64_t b, int64_t hq, int64_t hkv, int64_t s,
@@ -186,19 +189,19 @@ int pb_lmhead_ce_fwd(const void *x, int64_t ldx, const void *w, int64_t ldw, int
 /* Backward of pb_lmhead_ce_fwd (fused_ce.py:176-202), vocab chunk by vocab
  * chunk (vchunk rows of w, a multiple of 8):
  *   dL = (softmax*(1 + 2z*lse) - onehot) * grad_out   (bf16, one chunk)
- *   dx = sum over chunks dL w_chunk   (fp32 in dx_acc [n, d], row stride d;
- *                                      written to dx in dx_dtype at the end)
+ *   dx = sum over chunks dL w_chunk   (fp32 accumulation; dx in dx_dtype)
  *   dw[chunk] = dL^T x                (written in dw_dtype)
  * xt = x^T [d, >= n] and wt = w^T [d, >= v] (bf16, e.g. from pb_pack_bf16);
- * dl [n, ldl >= vchunk] and dlt [vchunk, ldlt >= n] are bf16 workspaces.
+ * workspace: pb_lmhead_ce_bwd_workspace_bytes(n, v, d, vchunk) bytes (the
+ * dlogits chunk in both layouts and fp32 dx accumulators).
  * grad_out is a device pointer to one fp32 (no host synchronisation).       */
+int64_t pb_lmhead_ce_bwd_workspace_bytes(int64_t n, int64_t v, int64_t d, int64_t vchunk);
 int pb_lmhead_ce_bwd(const void *x, int64_t ldx, const void *w, int64_t ldw, const void *xt,
                      int64_t ldxt, const void *wt, int64_t ldwt, int64_t n, int64_t v,
                      int64_t d, const int64_t *targets, int64_t ignore_index,
                      float z_loss_coeff, const float *lse, const float *grad_out,
-                     int64_t vchunk, void *dl, int64_t ldl, void *dlt, int64_t ldlt,
-                     float *dx_acc, void *dx, int dx_dtype, int64_t lddx, void *dw,
-                     int dw_dtype, int64_t lddw, void *stream);
+                     int64_t vchunk, void *workspace, void *dx, int dx_dtype, int64_t lddx,
+                     void *dw, int dw_dtype, int64_t lddw, void *stream);
 
 /* Layout helper of the CE path: dst (bf16) <- src (any float dtype), cast
  * and, if transpose, transposed; dst is [dst_rows, dst_cols] with row stride

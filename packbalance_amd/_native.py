@@ -67,7 +67,7 @@ SIGNATURES: dict[str, tuple] = {
         _i32,
         [_p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p],
     ),
-    "pb_attn_tile": (_i32, [_i32, _i64, _i32]),
+    "pb_attn_config": (_i32, [_i64, _i64, _i64, _i64, _i64, _p]),
     "pb_attn_plan": (_i32, [_p, _i64, _i64, _i64, _i64, _i64, _i32, _p, _p, _p, _p]),
     "pb_attn_fwd": (
         _i32,
@@ -82,15 +82,16 @@ SIGNATURES: dict[str, tuple] = {
     "pb_lmhead_ce_fwd": (
         _i32, [_p, _i64, _p, _i64, _i64, _i64, _i64, _p, _i64, _f32, _p, _p, _p, _p, _p],
     ),
+    "pb_lmhead_ce_bwd_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "pb_lmhead_ce_bwd": (
         _i32,
         [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _p, _i64, _f32, _p, _p,
-         _i64, _p, _i64, _p, _i64, _p, _p, _i32, _i64, _p, _i32, _i64, _p],
+         _i64, _p, _p, _i32, _i64, _p, _i32, _i64, _p],
     ),
     "pb_pack_bf16": (_i32, [_p, _i32, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i32, _p]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lib: C.CDLL | None = None
 _load_error: str | None = None

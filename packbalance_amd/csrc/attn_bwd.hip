@@ -6,34 +6,31 @@
 //   dV = P^T dO,  dP = dO V^T,  dS = P * (dP - D),
 //   dQ = scale * dS K,  dK = scale * dS^T Q.
 //
-// Three kernels, no atomics (results are run-to-run deterministic):
-//   attn_bwd_delta  D = rowsum(dO * O) per (pack, head, query).
-//   attn_bwd_dkdv   one workgroup per (pack, KV head, 128-row KV tile); wave w
-//                   owns 32 KV rows.  It walks every query head of its GQA group
-//                   and every 32-row query tile the plan lists for the KV tile,
-//                   so dK/dV accumulate in registers across the whole group.
-//                   S = Q K^T is computed with lane <-> KV row, which lets P^T
-//                   and dS^T feed the dV / dK MFMAs straight from the
-//                   accumulators; Q and dO are staged in LDS row-major (for S,
-//                   dP) and transposed (for dK, dV).
+// Two kernels, no atomics (results are run-to-run deterministic):
 //   attn_bwd_dq     one workgroup per (pack, query head, 128-row query tile),
-//                   shaped like the forward: lane <-> query row, recomputes S^T
-//                   and dP^T per 64-row KV tile and accumulates dQ^T = K^T dS^T.
+//                   shaped like the forward: lane <-> query row.  It first forms
+//                   D = rowsum(dO * O) from its register-resident rows (stored
+//                   for the second kernel), then recomputes S^T and dP^T per
+//                   64-row KV tile and accumulates dQ^T = K^T dS^T, reading K^T
+//                   fragments from the row-major K tile with ds_read_b64_tr_b16.
+//   attn_bwd_dkdv   one workgroup per (pack, KV head, KV tile of 32*W rows);
+//                   wave w owns 32 KV rows with K and V fragments in
+//                   registers.  It walks every query head of its GQA group and
+//                   every 64-row query tile the plan lists for the KV tile, so
+//                   dK/dV accumulate in registers across the whole group.  When
+//                   the grid would be too small to fill the GPU (AttnConfig
+//                   split), each query head gets its own workgroup and writes
+//                   fp32 partials that attn_bwd_reduce sums over the group.  S = Q K^T
+//                   is computed with lane <-> KV row, so P^T and dS^T feed the
+//                   dV / dK MFMAs straight from the accumulators; the Q^T / dO^T
+//                   operands are read from the row-major LDS tiles with
+//                   ds_read_b64_tr_b16, and the next tile is prefetched into
+//                   registers while the current one is computed.
 #include "attn_common.hpp"
 
 namespace pb {
 namespace attn {
 
-constexpr int kKvBN = 128;  // dK/dV kernel: KV rows per workgroup
-constexpr int kKvBM = 32;   // dK/dV kernel: query rows per step
-constexpr int kDqBM = 128;  // dQ kernel: query rows per workgroup
-constexpr int kDqBN = 64;   // dQ kernel: KV rows per step
-
-int attn_bwd_tile(int kernel, int which) {
-  if (kernel == 1) return which == 0 ? kKvBM : kKvBN;
-  if (kernel == 2) return which == 0 ? kDqBM : kDqBN;
-  return -1;
-}
 
 struct View {
   bf16_t *p;
@@ -51,60 +48,39 @@ struct BwdArgs {
   int64_t doc_sb;
   const int32_t *qcnt, *qlist;  // dQ plan (by query tile)
   const int32_t *kcnt, *klist;  // dK/dV plan (by KV tile)
+  float *dk_part, *dv_part;     // split: fp32 [B][Hq][S][D] partials
   int B, Hq, Hkv, S, D;
   int nqt_dq, nkt_dq, nqt_kv, nkt_kv;
   float sl2, scale;
   int vec;
 };
 
-// ---------------------------------------------------------------- delta
-// One thread per (b, s, h) row, h fastest: neighbouring threads read
-// neighbouring rows of the [B, S, H, D] memory the model produces.
-__global__ __launch_bounds__(256) void attn_bwd_delta(BwdArgs a) {
-  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t total = (int64_t)a.B * a.S * a.Hq;
-  if (t >= total) return;
-  const int h = (int)(t % a.Hq);
-  const int64_t s = (t / a.Hq) % a.S;
-  const int b = (int)(t / ((int64_t)a.Hq * a.S));
-  const bf16_t *o = a.o.row(b, h, s);
-  const bf16_t *g = a.dout.row(b, h, s);
-  float acc = 0.f;
-  if (a.vec) {
-    for (int d = 0; d < a.D; d += 8) {
-      const bf16x8_t x = *reinterpret_cast<const bf16x8_t *>(o + d);
-      const bf16x8_t y = *reinterpret_cast<const bf16x8_t *>(g + d);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc += (float)x[i] * (float)y[i];
-    }
-  } else {
-    for (int d = 0; d < a.D; ++d) acc += (float)o[d] * (float)g[d];
-  }
-  a.delta[((int64_t)b * a.Hq + h) * a.S + s] = acc;
-}
-
 // ---------------------------------------------------------------- dK, dV
-template <int DP>
-__global__ __launch_bounds__(256) void attn_bwd_dkdv(BwdArgs a) {
-  constexpr int BN = kKvBN, BM = kKvBM;
+template <int DP, int WAVES, bool SPLIT>
+__global__ __launch_bounds__(64 * WAVES) void attn_bwd_dkdv(BwdArgs a) {
+  constexpr int NT = 64 * WAVES;
+  constexpr int BN = 32 * WAVES, BM = kQStep;
   constexpr int QP = DP + 8;  // row-major pitch (elements)
-  constexpr int TP = BM + 4;  // transposed pitch (elements)
   constexpr int NDK = DP / 16, NDB = DP / 32, CH = DP / 8;
-  constexpr int NCH = BM * CH;  // 16-byte chunks of one [BM x DP] tile
+  constexpr int NCH = BM * CH;             // 16-byte chunks of one [BM x DP] tile
+  constexpr int NLD = (2 * NCH + NT - 1) / NT;  // chunks per thread (Q and dO)
   __shared__ __align__(16) bf16_t Qs[BM * QP];
-  __shared__ __align__(16) bf16_t Gs[BM * QP];  // dO, row-major
-  __shared__ __align__(16) bf16_t Qt[DP * TP];
-  __shared__ __align__(16) bf16_t Gt[DP * TP];  // dO, transposed
+  __shared__ __align__(16) bf16_t Gs[BM * QP];  // dO
   __shared__ float lse_s[BM], dlt_s[BM];
   __shared__ int64_t qdoc_s[BM];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hh = lane >> 5, l32 = lane & 31;
-  const int nbh = a.B * a.Hkv;
-  const int kt = (int)(blockIdx.x / nbh);  // early KV tiles are attended most: first
-  const int rem = (int)(blockIdx.x % nbh);
+  // Grid: (KV tile, pack, KV head[, group member]); early KV tiles are
+  // attended by the most query tiles, so they come first.
+  const int Gfull = a.Hq / a.Hkv;
+  const int G = SPLIT ? 1 : Gfull;
+  const int per_tile = a.B * a.Hkv * (SPLIT ? Gfull : 1);
+  const int kt = (int)(blockIdx.x / per_tile);
+  int rem = (int)(blockIdx.x % per_tile);
+  const int g0 = SPLIT ? rem % Gfull : 0;
+  if (SPLIT) rem /= Gfull;
   const int b = rem / a.Hkv, hk = rem - (rem / a.Hkv) * a.Hkv;
-  const int G = a.Hq / a.Hkv;
   const bool vec = a.vec != 0;
   const int64_t *docb = a.doc + b * a.doc_sb;
 
@@ -130,73 +106,91 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv(BwdArgs a) {
 
   const int cnt = a.kcnt[b * a.nkt_kv + kt];
   const int32_t *lst = a.klist + ((int64_t)b * a.nkt_kv + kt) * a.nqt_kv;
-  for (int g = 0; g < G; ++g) {
-    const int h = hk * G + g;
-    const float *lse_row = a.lse + ((int64_t)b * a.Hq + h) * a.S;
-    const float *dlt_row = a.delta + ((int64_t)b * a.Hq + h) * a.S;
-    for (int it = 0; it < cnt; ++it) {
-      const int e = lst[it];
-      const int q0 = plan_tile(e) * BM;
-      const bool full = plan_full(e);
-      __syncthreads();
-      for (int c = tid; c < 2 * NCH; c += 256) {
+  const int steps = cnt * G;  // (query head of the group, query tile) pairs
+
+  // Register prefetch of one step's Q / dO tiles and per-row scalars.
+  bf16x8_t pre[NLD];
+  float pre_lse = 0.f, pre_dlt = 0.f;
+  int64_t pre_doc = 0;
+  auto fetch = [&](int step) {
+    const int g = step / cnt, it = step - (step / cnt) * cnt;
+    const int h = hk * Gfull + g0 + g;
+    const int q0 = plan_tile(lst[it]) * BM;
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+      const int c = tid + NT * i;
+      if (c < 2 * NCH) {
         const int which = c / NCH, cc = c - which * NCH;
         const int row = cc / CH, col = (cc % CH) * 8;
         const int qr = q0 + row;
         const bool ok = qr < a.S;
         const View &src = which ? a.dout : a.q;
-        const bf16x8_t x = load_row8(src.row(b, h, ok ? qr : 0), col, a.D, ok, vec);
-        bf16_t *rm = which ? Gs : Qs;
-        bf16_t *tr = which ? Gt : Qt;
-        *reinterpret_cast<bf16x8_t *>(&rm[row * QP + col]) = x;
-#pragma unroll
-        for (int xi = 0; xi < 8; ++xi) tr[(col + xi) * TP + row] = x[xi];
+        pre[i] = load_row8(src.row(b, h, ok ? qr : 0), col, a.D, ok, vec);
       }
-      if (tid < BM) {
-        const int qr = q0 + tid;
-        const bool ok = qr < a.S;
-        lse_s[tid] = ok ? lse_row[qr] : 0.f;
-        dlt_s[tid] = ok ? dlt_row[qr] : 0.f;
-        qdoc_s[tid] = ok ? docb[qr] : 0;
-      }
-      __syncthreads();
+    }
+    for (int r = tid; r < BM; r += NT) {  // NT >= BM: one row per thread
+      const int qr = q0 + r;
+      const bool ok = qr < a.S;
+      const int64_t o = ((int64_t)b * a.Hq + h) * a.S + (ok ? qr : 0);
+      pre_lse = ok ? a.lse[o] : 0.f;
+      pre_dlt = ok ? a.delta[o] : 0.f;
+      pre_doc = ok ? docb[qr] : 0;
+    }
+  };
 
-      // S = Q K^T and dP = dO V^T for 32 query rows x this wave's 32 KV rows.
+  if (steps > 0) fetch(0);
+  for (int step = 0; step < steps; ++step) {
+    const int it = step % cnt;
+    const int e = lst[it];
+    const int q0 = plan_tile(e) * BM;
+    const bool full = plan_full(e);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+      const int c = tid + NT * i;
+      if (c < 2 * NCH) {
+        const int which = c / NCH, cc = c - which * NCH;
+        const int row = cc / CH, col = (cc % CH) * 8;
+        *reinterpret_cast<bf16x8_t *>(&(which ? Gs : Qs)[row * QP + col]) = pre[i];
+      }
+    }
+    if (tid < BM) {
+      lse_s[tid] = pre_lse;
+      dlt_s[tid] = pre_dlt;
+      qdoc_s[tid] = pre_doc;
+    }
+    __syncthreads();
+    if (step + 1 < steps) fetch(step + 1);
+
+    // S = Q K^T, dP = dO V^T: two 32-query blocks x this wave's 32 KV rows.
+    bf16x8_t pf[4], dsf[4];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
       f32x16_t sacc = zero16(), pacc = zero16();
 #pragma unroll
       for (int dk = 0; dk < NDK; ++dk) {
-        const bf16x8_t qa = *reinterpret_cast<const bf16x8_t *>(&Qs[l32 * QP + 16 * dk + 8 * hh]);
-        sacc = mfma32(qa, kf[dk], sacc);
-        const bf16x8_t ga = *reinterpret_cast<const bf16x8_t *>(&Gs[l32 * QP + 16 * dk + 8 * hh]);
-        pacc = mfma32(ga, vf[dk], pacc);
+        const int off = (32 * qb + l32) * QP + 16 * dk + 8 * hh;
+        sacc = mfma32(*reinterpret_cast<const bf16x8_t *>(&Qs[off]), kf[dk], sacc);
+        pacc = mfma32(*reinterpret_cast<const bf16x8_t *>(&Gs[off]), vf[dk], pacc);
       }
-      bf16x8_t pf[2], dsf[2];
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const int qr = 8 * (j >> 2) + 4 * hh + (j & 3);
+        const int qr = 32 * qb + 8 * (j >> 2) + 4 * hh + (j & 3);
         const int q = q0 + qr;
         const bool ok = full || (q < a.S && kvvalid && q >= kv && qdoc_s[qr] == kvdoc);
-        const float p = ok ? fast_exp2(sacc[j] * a.sl2 - lse_s[qr]) : 0.f;
-        const float ds = p * (pacc[j] - dlt_s[qr]);
-        pf[j >> 3][j & 7] = (bf16_t)p;
-        dsf[j >> 3][j & 7] = (bf16_t)ds;
+        const float p = ok ? fast_exp2(fmaf(sacc[j], a.sl2, -lse_s[qr])) : 0.f;
+        pf[2 * qb + (j >> 3)][j & 7] = (bf16_t)p;
+        dsf[2 * qb + (j >> 3)][j & 7] = (bf16_t)(p * (pacc[j] - dlt_s[qr]));
       }
-      // dV += P^T dO, dK += dS^T Q; B operands read the transposed tiles.
-#pragma unroll
-      for (int db = 0; db < NDB; ++db)
-#pragma unroll
-        for (int qk = 0; qk < 2; ++qk) {
-          const int off = (32 * db + l32) * TP + 16 * qk + 4 * hh;
-          const u32x2 g_lo = *reinterpret_cast<const u32x2 *>(&Gt[off]);
-          const u32x2 g_hi = *reinterpret_cast<const u32x2 *>(&Gt[off + 8]);
-          u32x4 gb = {g_lo[0], g_lo[1], g_hi[0], g_hi[1]};
-          dv_acc[db] = mfma32(pf[qk], *reinterpret_cast<bf16x8_t *>(&gb), dv_acc[db]);
-          const u32x2 q_lo = *reinterpret_cast<const u32x2 *>(&Qt[off]);
-          const u32x2 q_hi = *reinterpret_cast<const u32x2 *>(&Qt[off + 8]);
-          u32x4 qb = {q_lo[0], q_lo[1], q_hi[0], q_hi[1]};
-          dk_acc[db] = mfma32(dsf[qk], *reinterpret_cast<bf16x8_t *>(&qb), dk_acc[db]);
-        }
     }
+    // dV += P^T dO, dK += dS^T Q; B operands = column fragments of the tiles.
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int qk = 0; qk < 4; ++qk) {
+        dv_acc[db] = mfma32(pf[qk], lds_col_frag(Gs, QP, 16 * qk, 32 * db, lane), dv_acc[db]);
+        dk_acc[db] = mfma32(dsf[qk], lds_col_frag(Qs, QP, 16 * qk, 32 * db, lane), dk_acc[db]);
+      }
   }
   // Accumulators: lane <-> head-dim column, register j <-> KV row of the wave.
 #pragma unroll
@@ -207,24 +201,50 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv(BwdArgs a) {
     for (int j = 0; j < 16; ++j) {
       const int kvr = kt * BN + wave * 32 + 8 * (j >> 2) + 4 * hh + (j & 3);
       if (kvr < a.S) {
-        a.dk.row(b, hk, kvr)[d] = (bf16_t)(dk_acc[db][j] * a.scale);
-        a.dv.row(b, hk, kvr)[d] = (bf16_t)dv_acc[db][j];
+        if constexpr (SPLIT) {
+          const int64_t o = (((int64_t)b * a.Hq + hk * Gfull + g0) * a.S + kvr) * a.D + d;
+          a.dk_part[o] = dk_acc[db][j];
+          a.dv_part[o] = dv_acc[db][j];
+        } else {
+          a.dk.row(b, hk, kvr)[d] = (bf16_t)(dk_acc[db][j] * a.scale);
+          a.dv.row(b, hk, kvr)[d] = (bf16_t)dv_acc[db][j];
+        }
       }
     }
   }
 }
 
+// Split dK/dV: sum the fp32 partials of the G query heads of each KV head.
+__global__ __launch_bounds__(256) void attn_bwd_reduce(BwdArgs a) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t total = (int64_t)a.B * a.Hkv * a.S * a.D;
+  if (t >= total) return;
+  const int d = (int)(t % a.D);
+  const int64_t sidx = (t / a.D) % a.S;
+  const int hk = (int)((t / ((int64_t)a.D * a.S)) % a.Hkv);
+  const int b = (int)(t / ((int64_t)a.D * a.S * a.Hkv));
+  const int G = a.Hq / a.Hkv;
+  float sk = 0.f, sv = 0.f;
+  for (int g = 0; g < G; ++g) {
+    const int64_t o = (((int64_t)b * a.Hq + hk * G + g) * a.S + sidx) * a.D + d;
+    sk += a.dk_part[o];
+    sv += a.dv_part[o];
+  }
+  a.dk.row(b, hk, sidx)[d] = (bf16_t)(sk * a.scale);
+  a.dv.row(b, hk, sidx)[d] = (bf16_t)sv;
+}
+
 // ---------------------------------------------------------------- dQ
-template <int DP>
-__global__ __launch_bounds__(256) void attn_bwd_dq(BwdArgs a) {
-  constexpr int BM = kDqBM, BN = kDqBN;
-  constexpr int KP = DP + 8, VP = BN + 4;
+template <int DP, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void attn_bwd_dq(BwdArgs a) {
+  constexpr int NT = 64 * WAVES;
+  constexpr int BM = 32 * WAVES, BN = kKvStep;
+  constexpr int KP = DP + 8;
   constexpr int NDK = DP / 16, NDB = DP / 32, CH = DP / 8;
-  constexpr int NLD = BN * CH / 256;
-  static_assert(NLD >= 1 && BN * CH % 256 == 0, "tile/thread mismatch");
+  constexpr int NLD = BN * CH / NT;
+  static_assert(NLD >= 1 && BN * CH % NT == 0, "tile/thread mismatch");
   __shared__ __align__(16) bf16_t Ks[BN * KP];
   __shared__ __align__(16) bf16_t Vs[BN * KP];
-  __shared__ __align__(16) bf16_t Kt[DP * VP];
   __shared__ int64_t kdoc[BN];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -240,17 +260,25 @@ __global__ __launch_bounds__(256) void attn_bwd_dq(BwdArgs a) {
   const int qi = qt * BM + wave * 32 + l32;
   const bool qvalid = qi < a.S;
   const int64_t qdoc = qvalid ? docb[qi] : 0;
-  const float lse2 = qvalid ? a.lse[((int64_t)b * a.Hq + h) * a.S + qi] : 0.f;
-  const float dlt = qvalid ? a.delta[((int64_t)b * a.Hq + h) * a.S + qi] : 0.f;
+  const int64_t row_o = ((int64_t)b * a.Hq + h) * a.S + (qvalid ? qi : 0);
+  const float lse2 = qvalid ? a.lse[row_o] : 0.f;
   bf16x8_t qf[NDK], gf[NDK];
+  float dlt = 0.f;
   {
     const int64_t r = qvalid ? qi : 0;
     const bf16_t *qrow = a.q.row(b, h, r), *grow = a.dout.row(b, h, r);
+    const bf16_t *orow = a.o.row(b, h, r);
 #pragma unroll
     for (int dk = 0; dk < NDK; ++dk) {
       qf[dk] = load_row8(qrow, 16 * dk + 8 * hh, a.D, qvalid, vec);
       gf[dk] = load_row8(grow, 16 * dk + 8 * hh, a.D, qvalid, vec);
+      const bf16x8_t of = load_row8(orow, 16 * dk + 8 * hh, a.D, qvalid, vec);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) dlt += (float)gf[dk][i] * (float)of[i];
     }
+    // The two lane halves hold complementary 8-element slices of the row.
+    dlt += __shfl_xor(dlt, 32);
+    if (qvalid && hh == 0) a.delta[row_o] = dlt;
   }
   f32x16_t dq_acc[NDB];
 #pragma unroll
@@ -264,7 +292,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq(BwdArgs a) {
     const int kv0 = plan_tile(e) * BN;
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
-      const int c = tid + 256 * i;
+      const int c = tid + NT * i;
       const int row = c / CH, col = (c % CH) * 8;
       const int kvr = kv0 + row;
       const bool ok = kvr < a.S;
@@ -279,12 +307,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dq(BwdArgs a) {
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
-      const int c = tid + 256 * i;
+      const int c = tid + NT * i;
       const int row = c / CH, col = (c % CH) * 8;
       *reinterpret_cast<bf16x8_t *>(&Ks[row * KP + col]) = kr[i];
       *reinterpret_cast<bf16x8_t *>(&Vs[row * KP + col]) = vr[i];
-#pragma unroll
-      for (int x = 0; x < 8; ++x) Kt[(col + x) * VP + row] = kr[i][x];
     }
     if (tid < BN) kdoc[tid] = dr;
     __syncthreads();
@@ -307,7 +333,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq(BwdArgs a) {
         const int kr_ = 32 * blk + 8 * (j >> 2) + 4 * hh + (j & 3);
         const int kvr = kv0 + kr_;
         const bool ok = full || (qvalid && kvr <= qi && kvr < a.S && kdoc[kr_] == qdoc);
-        const float p = ok ? fast_exp2(sacc[j] * a.sl2 - lse2) : 0.f;
+        const float p = ok ? fast_exp2(fmaf(sacc[j], a.sl2, -lse2)) : 0.f;
         dsf[2 * blk + (j >> 3)][j & 7] = (bf16_t)(p * (pacc[j] - dlt));
       }
     }
@@ -315,13 +341,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq(BwdArgs a) {
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const bf16_t *krow = &Kt[(32 * db + l32) * VP + 16 * kk + 4 * hh];
-        const u32x2 lo = *reinterpret_cast<const u32x2 *>(krow);
-        const u32x2 hi = *reinterpret_cast<const u32x2 *>(krow + 8);
-        u32x4 ka = {lo[0], lo[1], hi[0], hi[1]};
-        dq_acc[db] = mfma32(*reinterpret_cast<bf16x8_t *>(&ka), dsf[kk], dq_acc[db]);
-      }
+      for (int kk = 0; kk < 4; ++kk)
+        dq_acc[db] = mfma32(lds_col_frag(Ks, KP, 16 * kk, 32 * db, lane), dsf[kk], dq_acc[db]);
   }
   if (!qvalid) return;
   bf16_t *qrow = a.dq.row(b, h, qi);
@@ -348,16 +369,30 @@ View view_of(const pb_bhsd *t) {
 }  // namespace attn
 }  // namespace pb
 
-extern "C" int pb_attn_tile(int kernel, int64_t head_dim, int which) {
-  (void)head_dim;
-  if (kernel == 0) return which == 0 ? pb::attn::kFwdBM : pb::attn::kFwdBN;
-  return pb::attn::attn_bwd_tile(kernel, which);
+extern "C" int pb_attn_config(int64_t b, int64_t hq, int64_t hkv, int64_t s, int64_t d,
+                              int64_t *out) {
+  using namespace pb::attn;
+  pb::clear_error();
+  if (b < 1 || hq < 1 || hkv < 1 || s < 1 || d < 1 || hq % hkv) {
+    pb::set_error("pb_attn_config: bad shape");
+    return PB_EINVAL;
+  }
+  const AttnConfig c = attn_config(b, hq, hkv, s, d);
+  out[0] = c.fwd_q_tile();
+  out[1] = kKvStep;
+  out[2] = kQStep;
+  out[3] = c.kv_tile();
+  out[4] = c.dq_q_tile();
+  out[5] = kKvStep;
+  out[6] = attn_bwd_workspace(b, hq, hkv, s, d);
+  out[7] = c.split;
+  return PB_OK;
 }
 
 extern "C" int pb_attn_bwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v,
                            const pb_bhsd *out, const pb_bhsd *dout, const pb_bhsd *dq,
                            const pb_bhsd *dk, const pb_bhsd *dv, const float *lse,
-                           float *delta_ws, const int64_t *doc_ids, int64_t doc_stride,
+                           void *workspace, const int64_t *doc_ids, int64_t doc_stride,
                            const int32_t *q_plan_counts, const int32_t *q_plan_lists,
                            const int32_t *kv_plan_counts, const int32_t *kv_plan_lists,
                            int64_t b, int64_t hq, int64_t hkv, int64_t s, int64_t d, float scale,
@@ -367,41 +402,54 @@ extern "C" int pb_attn_bwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v,
   clear_error();
   int rc = check_attn_shape("pb_attn_bwd", b, hq, hkv, s, d, dtype);
   if (rc) return rc;
-  PB_CHECK_ARG(q && k && v && out && dout && dq && dk && dv && lse && delta_ws && doc_ids &&
+  PB_CHECK_ARG(scale > 0.f, "pb_attn_bwd: softmax scale must be positive");
+  PB_CHECK_ARG(q && k && v && out && dout && dq && dk && dv && lse && workspace && doc_ids &&
                    q_plan_counts && q_plan_lists && kv_plan_counts && kv_plan_lists,
                "pb_attn_bwd: null argument");
+  const AttnConfig cfg = attn_config(b, hq, hkv, s, d);
   BwdArgs a;
   a.q = view_of(q); a.k = view_of(k); a.v = view_of(v); a.o = view_of(out);
   a.dout = view_of(dout); a.dq = view_of(dq); a.dk = view_of(dk); a.dv = view_of(dv);
   a.lse = lse;
-  a.delta = delta_ws;
+  char *ws = static_cast<char *>(workspace);
+  a.delta = reinterpret_cast<float *>(ws);
+  const int64_t delta_bytes = (b * hq * s * 4 + 255) / 256 * 256;
+  a.dk_part = reinterpret_cast<float *>(ws + delta_bytes);
+  a.dv_part = a.dk_part + b * hq * s * d;
   a.doc = doc_ids;
   a.doc_sb = doc_stride;
   a.qcnt = q_plan_counts; a.qlist = q_plan_lists;
   a.kcnt = kv_plan_counts; a.klist = kv_plan_lists;
   a.B = (int)b; a.Hq = (int)hq; a.Hkv = (int)hkv; a.S = (int)s; a.D = (int)d;
-  a.nqt_dq = (int)((s + kDqBM - 1) / kDqBM);
-  a.nkt_dq = (int)((s + kDqBN - 1) / kDqBN);
-  a.nqt_kv = (int)((s + kKvBM - 1) / kKvBM);
-  a.nkt_kv = (int)((s + kKvBN - 1) / kKvBN);
+  a.nqt_dq = (int)((s + cfg.dq_q_tile() - 1) / cfg.dq_q_tile());
+  a.nkt_dq = (int)((s + kKvStep - 1) / kKvStep);
+  a.nqt_kv = (int)((s + kQStep - 1) / kQStep);
+  a.nkt_kv = (int)((s + cfg.kv_tile() - 1) / cfg.kv_tile());
   a.sl2 = scale * kLog2e;
   a.scale = scale;
   a.vec = views_vectorizable(d, {q, k, v, out, dout, dq, dk, dv});
   hipStream_t st = as_stream(stream);
-  const int64_t rows = b * hq * s;
-  hipLaunchKernelGGL(attn_bwd_delta, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st, a);
-  rc = launch_status("pb_attn_bwd(delta)");
+  // dq first: it also writes delta = rowsum(dO * O), which dkdv reads.
+  dim3 g_q((unsigned)(a.nqt_dq * b * hq));
+  dim3 g_kv((unsigned)(a.nkt_kv * b * hkv * (cfg.split ? hq / hkv : 1)));
+#define PB_DQ(DP, W) hipLaunchKernelGGL((attn_bwd_dq<DP, W>), g_q, dim3(64 * W), 0, st, a)
+#define PB_KV(DP, W, SP) hipLaunchKernelGGL((attn_bwd_dkdv<DP, W, SP>), g_kv, dim3(64 * W), 0, st, a)
+#define PB_BY_D(M, ...) \
+  do { if (d <= 32) M(32, __VA_ARGS__); else if (d <= 64) M(64, __VA_ARGS__); else M(128, __VA_ARGS__); } while (0)
+  if (cfg.dq_waves == 4) PB_BY_D(PB_DQ, 4); else PB_BY_D(PB_DQ, 2);
+  rc = launch_status("pb_attn_bwd(dq)");
   if (rc) return rc;
-  dim3 g_kv((unsigned)(a.nkt_kv * b * hkv)), g_q((unsigned)(a.nqt_dq * b * hq));
-  if (d <= 32) {
-    hipLaunchKernelGGL(attn_bwd_dkdv<32>, g_kv, dim3(256), 0, st, a);
-    hipLaunchKernelGGL(attn_bwd_dq<32>, g_q, dim3(256), 0, st, a);
-  } else if (d <= 64) {
-    hipLaunchKernelGGL(attn_bwd_dkdv<64>, g_kv, dim3(256), 0, st, a);
-    hipLaunchKernelGGL(attn_bwd_dq<64>, g_q, dim3(256), 0, st, a);
-  } else {
-    hipLaunchKernelGGL(attn_bwd_dkdv<128>, g_kv, dim3(256), 0, st, a);
-    hipLaunchKernelGGL(attn_bwd_dq<128>, g_q, dim3(256), 0, st, a);
+  if (cfg.kv_waves == 4) PB_BY_D(PB_KV, 4, false);
+  else if (cfg.split) PB_BY_D(PB_KV, 2, true);
+  else PB_BY_D(PB_KV, 2, false);
+#undef PB_BY_D
+#undef PB_KV
+#undef PB_DQ
+  rc = launch_status("pb_attn_bwd(dkdv)");
+  if (rc) return rc;
+  if (cfg.split) {
+    const int64_t n = b * hkv * s * d;
+    hipLaunchKernelGGL(attn_bwd_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a);
   }
   return launch_status("pb_attn_bwd");
 }

@@ -18,9 +18,11 @@
 namespace pb {
 namespace attn {
 
-// Forward kernel tiles: query rows per workgroup, KV rows per step.
-constexpr int kFwdBM = 128;
-constexpr int kFwdBN = 64;
+// KV rows per step of the query-major kernels (forward, dQ); query rows per
+// step of the KV-major kernel (dK/dV).  Each wave owns 32 rows of the other
+// axis, and a workgroup has 2 or 4 waves (see AttnConfig).
+constexpr int kKvStep = 64;
+constexpr int kQStep = 64;
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
@@ -55,6 +57,32 @@ __device__ __forceinline__ bf16x8_t load_row8(const bf16_t *row, int d0, int d, 
   return r;
 }
 
+// MFMA operand fragment read "down the columns" of a row-major LDS tile with
+// ds_read_b64_tr_b16.  That instruction works on 16-lane groups: the 16
+// supplied 4-element chunks form M[16][4] and lane i of the group receives
+// M[i/4 + 4e][i%4], e = 0..3 (checked on the device).  With supplying lane j
+// pointing at row R + j/4, column c0 + 4(j%4), lane i receives rows R..R+3 of
+// column c0 + i.  Here the fragment for lane l is column col0 + l%32 and the
+// eight k slots are tile rows k0 + pi(h, s) (h = l/32): two reads, rows
+// k0 + 4h .. +3 (slots 0-3) and k0 + 8 + 4h .. +3 (slots 4-7).
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
+
+__device__ __forceinline__ bf16x8_t lds_col_frag(const bf16_t *tile, int pitch, int k0, int col0,
+                                                 int lane) {
+  const int j = lane & 15, g = lane >> 4, h = lane >> 5;
+  const int col = col0 + 16 * (g & 1) + 4 * (j & 3);
+  const int row = k0 + 4 * h + (j >> 2);
+  const bf16_t *p0 = tile + row * pitch + col;
+  const bf16_t *p1 = p0 + 8 * pitch;
+  // C-style casts: generic -> LDS address-space casts of pointers into __shared__ tiles.
+  const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(p0));
+  const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(p1));
+  typedef short i16x8_t __attribute__((ext_vector_type(8)));
+  i16x8_t r = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return *reinterpret_cast<bf16x8_t *>(&r);
+}
+
 // Packed plan entry: tile index << 1 | FULL flag.
 __device__ __forceinline__ int plan_tile(int e) { return e >> 1; }
 __device__ __forceinline__ bool plan_full(int e) { return e & 1; }
@@ -85,8 +113,40 @@ inline bool views_vectorizable(int64_t d, std::initializer_list<const pb_bhsd *>
   return true;
 }
 
-// Tile sizes of the backward kernels (attn_bwd.hip).
-int attn_bwd_tile(int kernel, int which);
+// Launch shape of the three kernels for one problem size.  A workgroup of W
+// waves covers 32*W rows; 4 waves amortise each staged tile over more MFMAs,
+// 2 waves double the grid when the problem is small (one 2048-token pack has
+// only 12 heads x 16 query tiles).  When even that leaves the dK/dV grid
+// short, every query head of a GQA group gets its own workgroup and writes an
+// fp32 partial that a small kernel sums (split).
+struct AttnConfig {
+  int fwd_waves, dq_waves, kv_waves, split;
+  int fwd_q_tile() const { return 32 * fwd_waves; }
+  int dq_q_tile() const { return 32 * dq_waves; }
+  int kv_tile() const { return 32 * kv_waves; }
+};
+
+inline AttnConfig attn_config(int64_t b, int64_t hq, int64_t hkv, int64_t s, int64_t d) {
+  (void)d;
+  const int64_t kFill = 512;  // two workgroups per CU on 256 CUs
+  auto tiles = [&](int rows) { return (s + rows - 1) / rows; };
+  AttnConfig c;
+  c.fwd_waves = b * hq * tiles(128) >= kFill ? 4 : 2;
+  c.dq_waves = c.fwd_waves;
+  c.kv_waves = b * hkv * tiles(128) >= kFill ? 4 : 2;
+  c.split = (c.kv_waves == 2 && b * hkv * tiles(64) < kFill && hq > hkv) ? 1 : 0;
+  return c;
+}
+
+// Workspace of pb_attn_bwd: delta [b, hq, s] fp32, then (split) dK and dV
+// partials [b, hq, s, d] fp32 each.
+inline int64_t attn_bwd_workspace(int64_t b, int64_t hq, int64_t hkv, int64_t s, int64_t d) {
+  const AttnConfig c = attn_config(b, hq, hkv, s, d);
+  int64_t bytes = b * hq * s * 4;
+  bytes = (bytes + 255) / 256 * 256;
+  if (c.split) bytes += 2 * b * hq * s * d * 4;
+  return bytes;
+}
 
 }  // namespace attn
 

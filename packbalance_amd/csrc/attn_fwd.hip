@@ -4,20 +4,21 @@
 // runs with the document BlockMask (mask doc[q] == doc[kv] && q >= kv, GQA
 // query head h -> KV head h / (Hq/Hkv), scale 1/sqrt(D)).
 //
-// Work decomposition: one 256-thread workgroup per (pack, query head, 128-row
-// query tile); each of its 4 waves owns 32 query rows.  The workgroup walks
-// only the KV tiles (64 rows) that the tile plan lists for its query tile --
-// tiles with no same-document causal pair are never loaded -- and applies the
-// element mask only on PARTIAL tiles.
+// Work decomposition: one workgroup per (pack, query head, query tile of
+// 32*W rows) with W = 2 or 4 waves of 32 query rows each (AttnConfig picks W
+// from the grid size).  The workgroup walks only the KV tiles (64 rows) that
+// the tile plan lists for its query tile -- tiles with no same-document causal
+// pair are never loaded -- and applies the element mask only on PARTIAL tiles.
 //
 // Per KV tile a wave computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16, so a
 // lane owns one query column: the online-softmax max/sum are lane-local plus
 // one exchange with lane^32, and the O^T accumulator of a lane belongs to a
 // single query (one rescale factor per lane).  P^T leaves the accumulators as
 // the B operand of O^T += V^T P^T directly (see attn_common.hpp for the k-slot
-// permutation), so P never touches LDS.  K is staged row-major and V
-// transposed in LDS; the next tile's K/V are prefetched into registers while
-// the current one is computed.
+// permutation), so P never touches LDS.  K and V are staged row-major in LDS;
+// V^T fragments come from the transposing LDS load ds_read_b64_tr_b16.  The
+// next tile's K/V are prefetched into registers while the current one is
+// computed.
 #include "attn_common.hpp"
 
 namespace pb {
@@ -42,18 +43,18 @@ struct FwdArgs {
   int vec;    // 16-byte global access allowed
 };
 
-template <int DP>
-__global__ __launch_bounds__(256) void attn_fwd_kernel(FwdArgs a) {
-  constexpr int BM = kFwdBM, BN = kFwdBN;
-  constexpr int KP = DP + 8;  // K row pitch in LDS (elements)
-  constexpr int VP = BN + 4;  // V^T row pitch in LDS (elements)
+template <int DP, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void attn_fwd_kernel(FwdArgs a) {
+  constexpr int NT = 64 * WAVES;
+  constexpr int BM = 32 * WAVES, BN = kKvStep;
+  constexpr int KP = DP + 8;  // K / V row pitch in LDS (elements)
   constexpr int NDK = DP / 16;
   constexpr int NDB = DP / 32;
   constexpr int CH = DP / 8;              // 16-byte chunks per K/V row
-  constexpr int NLD = BN * CH / 256;      // chunks per thread per tile
-  static_assert(NLD >= 1 && BN * CH % 256 == 0, "tile/thread mismatch");
+  constexpr int NLD = BN * CH / NT;       // chunks per thread per tile
+  static_assert(NLD >= 1 && BN * CH % NT == 0, "tile/thread mismatch");
   __shared__ __align__(16) bf16_t Ks[BN * KP];
-  __shared__ __align__(16) bf16_t Vt[DP * VP];
+  __shared__ __align__(16) bf16_t Vs[BN * KP];
   __shared__ int64_t kdoc[BN];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -97,7 +98,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(FwdArgs a) {
     const int kv0 = plan_tile(e) * BN;
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
-      const int c = tid + 256 * i;
+      const int c = tid + NT * i;
       const int row = c / CH, col = (c % CH) * 8;
       const int kv = kv0 + row;
       const bool ok = kv < a.S;
@@ -114,11 +115,10 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(FwdArgs a) {
     __syncthreads();  // every wave is done reading the previous tile
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
-      const int c = tid + 256 * i;
+      const int c = tid + NT * i;
       const int row = c / CH, col = (c % CH) * 8;
       *reinterpret_cast<bf16x8_t *>(&Ks[row * KP + col]) = kr[i];
-#pragma unroll
-      for (int x = 0; x < 8; ++x) Vt[(col + x) * VP + row] = vr[i][x];
+      *reinterpret_cast<bf16x8_t *>(&Vs[row * KP + col]) = vr[i];
     }
     if (tid < BN) kdoc[tid] = dr;
     __syncthreads();
@@ -138,22 +138,25 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(FwdArgs a) {
     }
     const int kv0 = plan_tile(e) * BN;
     const bool full = plan_full(e);
+    // Running max kept in the log2-scaled domain; the per-element scale is
+    // folded into the exp2 argument (one FMA per score).
     float mloc = -INFINITY;
+    if (!full) {
 #pragma unroll
-    for (int blk = 0; blk < 2; ++blk)
+      for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        float x = sacc[blk][j] * a.sl2;
-        if (!full) {
+        for (int j = 0; j < 16; ++j) {
           const int kr_ = 32 * blk + 8 * (j >> 2) + 4 * hh + (j & 3);
           const int kv = kv0 + kr_;
           const bool ok = qvalid && kv <= qi && kv < a.S && kdoc[kr_] == qdoc;
-          x = ok ? x : -INFINITY;
+          sacc[blk][j] = ok ? sacc[blk][j] : -INFINITY;
         }
-        sacc[blk][j] = x;
-        mloc = fmaxf(mloc, x);
-      }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+    }
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) mloc = fmaxf(mloc, sacc[blk][j]);
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32)) * a.sl2;
     const float m_new = fmaxf(m, mloc);
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
     const float alpha = fast_exp2(m - m_use);
@@ -169,22 +172,18 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(FwdArgs a) {
     for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const float p = fast_exp2(sacc[blk][j] - m_use);
+        const float p = fast_exp2(fmaf(sacc[blk][j], a.sl2, -m_use));
         l += p;
         pf[2 * blk + (j >> 3)][j & 7] = (bf16_t)p;
       }
 
-    // O^T += V^T P^T; A = V^T rows d, k slots kv = 16kk + pi(hh, s).
+    // O^T += V^T P^T; A = V^T rows d, k slots kv = 16kk + pi(hh, s), read
+    // from the row-major V tile with the transposing LDS load.
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const bf16_t *vrow = &Vt[(32 * db + l32) * VP + 16 * kk + 4 * hh];
-        const u32x2 lo = *reinterpret_cast<const u32x2 *>(vrow);
-        const u32x2 hi = *reinterpret_cast<const u32x2 *>(vrow + 8);
-        u32x4 va4 = {lo[0], lo[1], hi[0], hi[1]};
-        oacc[db] = mfma32(*reinterpret_cast<bf16x8_t *>(&va4), pf[kk], oacc[db]);
-      }
+      for (int kk = 0; kk < 4; ++kk)
+        oacc[db] = mfma32(lds_col_frag(Vs, KP, 16 * kk, 32 * db, lane), pf[kk], oacc[db]);
   }
 
   const float l_tot = l + __shfl_xor(l, 32);
@@ -231,6 +230,7 @@ extern "C" int pb_attn_fwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v,
   if (rc) return rc;
   PB_CHECK_ARG(q && k && v && out && lse && doc_ids && plan_counts && plan_lists,
                "pb_attn_fwd: null argument");
+  PB_CHECK_ARG(scale > 0.f, "pb_attn_fwd: softmax scale must be positive");
   FwdArgs a;
   a.q = static_cast<const bf16_t *>(q->data);
   a.q_sb = q->stride_b; a.q_sh = q->stride_h; a.q_ss = q->stride_s;
@@ -246,17 +246,19 @@ extern "C" int pb_attn_fwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v,
   a.cnt = plan_counts;
   a.list = plan_lists;
   a.B = (int)b; a.Hq = (int)hq; a.Hkv = (int)hkv; a.S = (int)s; a.D = (int)d;
-  a.nqt = (int)((s + kFwdBM - 1) / kFwdBM);
-  a.nkt = (int)((s + kFwdBN - 1) / kFwdBN);
+  const AttnConfig cfg = attn_config(b, hq, hkv, s, d);
+  a.nqt = (int)((s + cfg.fwd_q_tile() - 1) / cfg.fwd_q_tile());
+  a.nkt = (int)((s + kKvStep - 1) / kKvStep);
   a.sl2 = scale * kLog2e;
   a.vec = views_vectorizable(d, {q, k, v, out});
   dim3 grid((unsigned)(a.nqt * b * hq));
   hipStream_t st = as_stream(stream);
-  if (d <= 32)
-    hipLaunchKernelGGL(attn_fwd_kernel<32>, grid, dim3(256), 0, st, a);
-  else if (d <= 64)
-    hipLaunchKernelGGL(attn_fwd_kernel<64>, grid, dim3(256), 0, st, a);
-  else
-    hipLaunchKernelGGL(attn_fwd_kernel<128>, grid, dim3(256), 0, st, a);
+#define PB_FWD(DP, W) hipLaunchKernelGGL((attn_fwd_kernel<DP, W>), grid, dim3(64 * W), 0, st, a)
+  if (cfg.fwd_waves == 4) {
+    if (d <= 32) PB_FWD(32, 4); else if (d <= 64) PB_FWD(64, 4); else PB_FWD(128, 4);
+  } else {
+    if (d <= 32) PB_FWD(32, 2); else if (d <= 64) PB_FWD(64, 2); else PB_FWD(128, 2);
+  }
+#undef PB_FWD
   return launch_status("pb_attn_fwd");
 }

@@ -57,6 +57,10 @@ struct GemmArgs {
   int64_t ldc, ldo;
   int out_dtype;
   int first, last;
+  // kAccum split-K: blockIdx.y = split; each split covers k_per_split of K and
+  // writes fp32 partials part[split][M][N]; split_reduce folds them.
+  int k_per_split;
+  float *part;
 };
 
 __device__ __forceinline__ f32x16_t zero16() {
@@ -104,6 +108,9 @@ __global__ __launch_bounds__(256) void gemm_nt(GemmArgs g) {
   const int ntm = (g.M + BM - 1) / BM;
   const int tm = blockIdx.x % ntm, tn = blockIdx.x / ntm;
   const int m0 = tm * BM, n0 = tn * BN;
+  // K range of this workgroup (all of K unless split-K).
+  const int kb = MODE == kAccum && g.part ? blockIdx.y * g.k_per_split : 0;
+  const int ke = MODE == kAccum && g.part ? min(g.K, kb + g.k_per_split) : g.K;
 
   f32x16_t acc[2][2];
 #pragma unroll
@@ -120,13 +127,13 @@ __global__ __launch_bounds__(256) void gemm_nt(GemmArgs g) {
       const int row = c >> 3, kc = (c & 7) * 8;
       const int k = k0 + kc;
       const int am = m0 + row, bn = n0 + row;
-      ra[i] = load8(g.A + (int64_t)(am < g.M ? am : 0) * g.lda, k, g.K, am < g.M);
-      rb[i] = load8(g.B + (int64_t)(bn < g.N ? bn : 0) * g.ldb, k, g.K, bn < g.N);
+      ra[i] = load8(g.A + (int64_t)(am < g.M ? am : 0) * g.lda, k, ke, am < g.M);
+      rb[i] = load8(g.B + (int64_t)(bn < g.N ? bn : 0) * g.ldb, k, ke, bn < g.N);
     }
   };
 
-  const int nk = (g.K + BK - 1) / BK;
-  fetch(0);
+  const int nk = (ke - kb + BK - 1) / BK;
+  fetch(kb);
   for (int kt = 0; kt < nk; ++kt) {
     __syncthreads();
 #pragma unroll
@@ -137,7 +144,7 @@ __global__ __launch_bounds__(256) void gemm_nt(GemmArgs g) {
       *reinterpret_cast<bf16x8_t *>(&Bs[row * AP + kc]) = rb[i];
     }
     __syncthreads();
-    if (kt + 1 < nk) fetch((kt + 1) * BK);
+    if (kt + 1 < nk) fetch(kb + (kt + 1) * BK);
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       bf16x8_t a[2], b[2];
@@ -253,6 +260,10 @@ __global__ __launch_bounds__(256) void gemm_nt(GemmArgs g) {
           if (m >= g.M) continue;
           float v = acc[i][j][r];
           if constexpr (MODE == kAccum) {
+            if (g.part) {
+              g.part[((int64_t)blockIdx.y * g.M + m) * g.N + n] = v;
+              continue;
+            }
             float *p = g.acc + (int64_t)m * g.ldc + n;
             if (!g.first) v += *p;
             if (g.last)
@@ -267,19 +278,50 @@ __global__ __launch_bounds__(256) void gemm_nt(GemmArgs g) {
   }
 }
 
+// out (+)= sum of the split-K partials (the kAccum epilogue, applied after a
+// split-K GEMM): fp32 accumulator in between chunks, out dtype at the end.
+__global__ __launch_bounds__(256) void split_reduce(GemmArgs g, int splits) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (int64_t)g.M * g.N) return;
+  const int m = (int)(t / g.N), n = (int)(t - (t / g.N) * g.N);
+  float v = 0.f;
+  for (int sidx = 0; sidx < splits; ++sidx) v += g.part[(int64_t)sidx * g.M * g.N + t];
+  float *p = g.acc + (int64_t)m * g.ldc + n;
+  if (!g.first) v += *p;
+  if (g.last)
+    store_out(g.out, g.out_dtype, (int64_t)m * g.ldo + n, v);
+  else
+    *p = v;
+}
+
 // Merge the per-tile partials of every token: lse (natural log) and row loss.
-__global__ __launch_bounds__(256) void lse_combine(const float *__restrict__ part_m,
-                                                   const float *__restrict__ part_s, int ntiles,
-                                                   int n, const float *__restrict__ tgt,
-                                                   const int64_t *__restrict__ targets,
-                                                   int64_t ignore_index, int v, float z,
-                                                   float *__restrict__ lse_out,
-                                                   float *__restrict__ loss) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= n) return;
+// Block = 64 tokens x 16 partial-tile groups; the 16 groups are merged in LDS.
+__global__ __launch_bounds__(1024) void lse_combine(const float *__restrict__ part_m,
+                                                    const float *__restrict__ part_s, int ntiles,
+                                                    int n, const float *__restrict__ tgt,
+                                                    const int64_t *__restrict__ targets,
+                                                    int64_t ignore_index, int v, float z,
+                                                    float *__restrict__ lse_out,
+                                                    float *__restrict__ loss) {
+  __shared__ float rm[16][64], rs[16][64];
+  const int lane = threadIdx.x & 63, grp = threadIdx.x >> 6;
+  const int i = blockIdx.x * 64 + lane;
   float m = -INFINITY, s = 0.f;
-  for (int t = 0; t < ntiles; ++t) {
-    const float m2 = part_m[(int64_t)t * n + i], s2 = part_s[(int64_t)t * n + i];
+  if (i < n) {
+    for (int t = grp; t < ntiles; t += 16) {
+      const float m2 = part_m[(int64_t)t * n + i], s2 = part_s[(int64_t)t * n + i];
+      const float mn = fmaxf(m, m2);
+      if (mn == -INFINITY) continue;
+      s = s * fast_exp2(m - mn) + s2 * fast_exp2(m2 - mn);
+      m = mn;
+    }
+  }
+  rm[grp][lane] = m;
+  rs[grp][lane] = s;
+  __syncthreads();
+  if (grp != 0 || i >= n) return;
+  for (int g = 1; g < 16; ++g) {
+    const float m2 = rm[g][lane], s2 = rs[g][lane];
     const float mn = fmaxf(m, m2);
     if (mn == -INFINITY) continue;
     s = s * fast_exp2(m - mn) + s2 * fast_exp2(m2 - mn);
@@ -428,20 +470,57 @@ extern "C" int pb_lmhead_ce_fwd(const void *x, int64_t ldx, const void *w, int64
   hipLaunchKernelGGL(gemm_nt<kLse>, dim3(tiles(g.M, g.N)), dim3(256), 0, st, g);
   int rc = launch_status("pb_lmhead_ce_fwd(gemm)");
   if (rc) return rc;
-  hipLaunchKernelGGL(lse_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g.part_m,
+  hipLaunchKernelGGL(lse_combine, dim3((unsigned)((n + 63) / 64)), dim3(1024), 0, st, g.part_m,
                      g.part_s, nmt, (int)n, g.tgt, targets, ignore_index, (int)v, z_loss_coeff, lse,
                      loss_rows);
   hipLaunchKernelGGL(sum_rows, dim3(1), dim3(1024), 0, st, loss_rows, (int)n, loss_sum);
   return launch_status("pb_lmhead_ce_fwd");
 }
 
+namespace {
+// Backward workspace: dL [n][vchunk] bf16, dL^T [vchunk][n8] bf16, the fp32
+// dx accumulator [n][d], the split-K partials [splits][n][d] (256-byte aligned
+// pieces).
+struct BwdWs {
+  int64_t ldl, ldlt, off_dlt, off_acc, off_part, bytes;
+  int splits, k_per_split;
+};
+
+BwdWs bwd_ws(int64_t n, int64_t v, int64_t d, int64_t vchunk) {
+  auto al = [](int64_t x) { return (x + 255) / 256 * 256; };
+  BwdWs w;
+  w.ldl = vchunk;
+  w.ldlt = (n + 7) / 8 * 8;
+  w.off_dlt = al(n * vchunk * 2);
+  w.off_acc = w.off_dlt + al(vchunk * w.ldlt * 2);
+  w.off_part = w.off_acc + al(n * d * 4);
+  // Split the dx GEMM's K (vocab chunk) when its tile grid cannot fill the GPU.
+  const int64_t tiles = ((n + pb::ce::BM - 1) / pb::ce::BM) * ((d + pb::ce::BN - 1) / pb::ce::BN);
+  int64_t splits = (512 + tiles - 1) / tiles;
+  const int64_t kmin = 1024;
+  if (splits > vchunk / kmin) splits = vchunk / kmin;
+  if (splits > 8) splits = 8;
+  if (splits < 1) splits = 1;
+  w.splits = (int)splits;
+  w.k_per_split = (int)(((vchunk + splits - 1) / splits + pb::ce::BK - 1) / pb::ce::BK * pb::ce::BK);
+  w.bytes = w.off_part + (splits > 1 ? al(splits * n * d * 4) : 0);
+  return w;
+}
+}  // namespace
+
+extern "C" int64_t pb_lmhead_ce_bwd_workspace_bytes(int64_t n, int64_t v, int64_t d,
+                                                    int64_t vchunk) {
+  if (n <= 0 || v <= 0 || d <= 0 || vchunk <= 0) return 0;
+  return bwd_ws(n, v, d, vchunk).bytes;
+}
+
 extern "C" int pb_lmhead_ce_bwd(const void *x, int64_t ldx, const void *w, int64_t ldw,
                                 const void *xt, int64_t ldxt, const void *wt, int64_t ldwt,
                                 int64_t n, int64_t v, int64_t d, const int64_t *targets,
                                 int64_t ignore_index, float z_loss_coeff, const float *lse,
-                                const float *grad_out, int64_t vchunk, void *dl, int64_t ldl,
-                                void *dlt, int64_t ldlt, float *dx_acc, void *dx, int dx_dtype,
-                                int64_t lddx, void *dw, int dw_dtype, int64_t lddw, void *stream) {
+                                const float *grad_out, int64_t vchunk, void *workspace, void *dx,
+                                int dx_dtype, int64_t lddx, void *dw, int dw_dtype, int64_t lddw,
+                                void *stream) {
   using namespace pb;
   using namespace pb::ce;
   clear_error();
@@ -449,12 +528,19 @@ extern "C" int pb_lmhead_ce_bwd(const void *x, int64_t ldx, const void *w, int64
   PB_CHECK_SUPPORTED(n < (1LL << 31) && v < (1LL << 31) && d < (1LL << 31),
                      "pb_lmhead_ce_bwd: too large");
   PB_CHECK_ARG(valid_dtype(dx_dtype) && valid_dtype(dw_dtype), "pb_lmhead_ce_bwd: bad dtype");
-  PB_CHECK_ARG(k_aligned(x, ldx) && k_aligned(w, ldw) && k_aligned(xt, ldxt) &&
-                   k_aligned(wt, ldwt) && k_aligned(dl, ldl) && k_aligned(dlt, ldlt) && d % 8 == 0,
-               "pb_lmhead_ce_bwd: operands must be 16-byte aligned with row strides %% 8 == 0");
   PB_CHECK_ARG(vchunk % 8 == 0, "pb_lmhead_ce_bwd: vchunk must be a multiple of 8");
-  PB_CHECK_ARG(ldl >= vchunk && ldlt >= n && ldxt >= n && ldwt >= v && lddx >= d && lddw >= d,
+  PB_CHECK_ARG(k_aligned(x, ldx) && k_aligned(w, ldw) && k_aligned(xt, ldxt) &&
+                   k_aligned(wt, ldwt) && k_aligned(workspace, 8) && d % 8 == 0,
+               "pb_lmhead_ce_bwd: operands must be 16-byte aligned with row strides %% 8 == 0");
+  PB_CHECK_ARG(ldxt >= n && ldwt >= v && lddx >= d && lddw >= d,
                "pb_lmhead_ce_bwd: row strides too small");
+  const BwdWs L = bwd_ws(n, v, d, vchunk);
+  char *wsb = static_cast<char *>(workspace);
+  bf16_t *dl = reinterpret_cast<bf16_t *>(wsb);
+  bf16_t *dlt = reinterpret_cast<bf16_t *>(wsb + L.off_dlt);
+  float *dx_acc = reinterpret_cast<float *>(wsb + L.off_acc);
+  float *part = L.splits > 1 ? reinterpret_cast<float *>(wsb + L.off_part) : nullptr;
+  const int64_t ldl = L.ldl, ldlt = L.ldlt;
   hipStream_t st = as_stream(stream);
   const int64_t nchunks = (v + vchunk - 1) / vchunk;
   for (int64_t c = 0; c < nchunks; ++c) {
@@ -473,8 +559,8 @@ extern "C" int pb_lmhead_ce_bwd(const void *x, int64_t ldx, const void *w, int64
     g.z = z_loss_coeff;
     g.lse = lse;
     g.grad_out = grad_out;
-    g.dl = static_cast<bf16_t *>(dl);
-    g.dlt = static_cast<bf16_t *>(dlt);
+    g.dl = dl;
+    g.dlt = dlt;
     g.ldl = ldl;
     g.ldlt = ldlt;
     hipLaunchKernelGGL(gemm_nt<kDlogits>, dim3(tiles(g.M, g.N)), dim3(256), 0, st, g);
@@ -482,7 +568,7 @@ extern "C" int pb_lmhead_ce_bwd(const void *x, int64_t ldx, const void *w, int64
     if (rc) return rc;
     // 2) dx (+)= dL W_chunk: A = dL [n][vc], B = W^T[:, v0:v0+vc] rows d.
     GemmArgs gx = {};
-    gx.A = static_cast<const bf16_t *>(dl);
+    gx.A = dl;
     gx.lda = ldl;
     gx.B = static_cast<const bf16_t *>(wt) + v0;
     gx.ldb = ldwt;
@@ -494,10 +580,18 @@ extern "C" int pb_lmhead_ce_bwd(const void *x, int64_t ldx, const void *w, int64
     gx.out_dtype = dx_dtype;
     gx.first = c == 0;
     gx.last = c == nchunks - 1;
-    hipLaunchKernelGGL(gemm_nt<kAccum>, dim3(tiles(gx.M, gx.N)), dim3(256), 0, st, gx);
+    gx.part = part;
+    gx.k_per_split = L.k_per_split;
+    const int splits = part ? (vc + L.k_per_split - 1) / L.k_per_split : 1;
+    hipLaunchKernelGGL(gemm_nt<kAccum>, dim3(tiles(gx.M, gx.N), splits), dim3(256), 0, st, gx);
+    if (part) {
+      const int64_t cnt = (int64_t)gx.M * gx.N;
+      hipLaunchKernelGGL(split_reduce, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, st, gx,
+                         splits);
+    }
     // 3) dW[v0:v0+vc] = dL^T x: A = dL^T [vc][n], B = x^T rows d.
     GemmArgs gw = {};
-    gw.A = static_cast<const bf16_t *>(dlt);
+    gw.A = dlt;
     gw.lda = ldlt;
     gw.B = static_cast<const bf16_t *>(xt);
     gw.ldb = ldxt;

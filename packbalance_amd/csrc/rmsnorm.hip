@@ -134,8 +134,28 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_reg(
 
   const int64_t r0 = (int64_t)blockIdx.x * rows_per_wg;
   const int64_t r1 = r0 + rows_per_wg < rows ? r0 + rows_per_wg : rows;
+  // Raw 16-byte vectors of the next row, loaded while this row is computed.
+  u32x4 nx[NV], nd[NV];
+  auto prefetch = [&](int64_t row) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = (i * 64 + lane) * VEC;
+      if (c < n) {
+        nx[i] = *reinterpret_cast<const u32x4 *>(x + row * xs + c);
+        nd[i] = *reinterpret_cast<const u32x4 *>(dy + row * dys + c);
+      }
+    }
+  };
+  if (r0 + wave < r1) prefetch(r0 + wave);
   for (int64_t row = r0 + wave; row < r1; row += kWaves) {
     const float r = rstd[row];
+    u32x4 cx[NV], cd[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      cx[i] = nx[i];
+      cd[i] = nd[i];
+    }
+    if (row + kWaves < r1) prefetch(row + kWaves);
     float xh[NV][VEC], g[NV][VEC];
     float dot = 0.f;
 #pragma unroll
@@ -143,8 +163,13 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_reg(
       const int c = (i * 64 + lane) * VEC;
       if (c < n) {
         float dv[VEC], wv[VEC];
-        load_vec<TX, VEC>(x + row * xs + c, xh[i]);
-        load_vec<TX, VEC>(dy + row * dys + c, dv);
+        const TX *ex = reinterpret_cast<const TX *>(&cx[i]);
+        const TX *ed = reinterpret_cast<const TX *>(&cd[i]);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          xh[i][e] = to_f32(ex[e]);
+          dv[e] = to_f32(ed[e]);
+        }
         load_vec<TW, VEC>(w + c, wv);
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
@@ -232,20 +257,33 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_loop(
   }
 }
 
-// dw[c] = sum_p partial[p, c]; 64 columns x 4 partial-row groups per block.
+// dw[c] = sum_p partial[p, c]: 64 columns x 16 partial-row groups per block,
+// each thread with four independent accumulators so the loads overlap.
 template <typename TW>
-__global__ __launch_bounds__(256) void rmsnorm_dw_reduce(const float *__restrict__ partial,
-                                                         TW *__restrict__ dw, int nparts, int n) {
-  __shared__ float red[4][64];
-  const int col = blockIdx.x * 64 + (threadIdx.x & 63);
-  const int grp = threadIdx.x >> 6;
-  float s = 0.f;
-  if (col < n)
-    for (int p = grp; p < nparts; p += 4) s += partial[(int64_t)p * n + col];
-  red[grp][threadIdx.x & 63] = s;
+__global__ __launch_bounds__(1024) void rmsnorm_dw_reduce(const float *__restrict__ partial,
+                                                          TW *__restrict__ dw, int nparts, int n) {
+  __shared__ float red[16][64];
+  const int lane = threadIdx.x & 63, grp = threadIdx.x >> 6;
+  const int col = blockIdx.x * 64 + lane;
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  if (col < n) {
+    int p = grp;
+    for (; p + 48 < nparts; p += 64) {
+      s0 += partial[(int64_t)p * n + col];
+      s1 += partial[(int64_t)(p + 16) * n + col];
+      s2 += partial[(int64_t)(p + 32) * n + col];
+      s3 += partial[(int64_t)(p + 48) * n + col];
+    }
+    for (; p < nparts; p += 16) s0 += partial[(int64_t)p * n + col];
+  }
+  red[grp][lane] = (s0 + s1) + (s2 + s3);
   __syncthreads();
-  if (grp == 0 && col < n) dw[col] = from_f32<TW>(red[0][threadIdx.x] + red[1][threadIdx.x] +
-                                                  red[2][threadIdx.x] + red[3][threadIdx.x]);
+  if (grp == 0 && col < n) {
+    float t = 0.f;
+#pragma unroll
+    for (int g = 0; g < 16; ++g) t += red[g][lane];
+    dw[col] = from_f32<TW>(t);
+  }
 }
 
 // ---------------------------------------------------------------- dispatch
@@ -256,9 +294,10 @@ struct BwdPlan {
 
 BwdPlan bwd_plan(int64_t rows) {
   // Aim for ~1024 workgroups (4 per CU) so the partial rows stay a small
-  // fraction of the traffic; never fewer than kWaves rows per workgroup.
+  // fraction of the traffic; at least 2 rows per wave so the next-row
+  // prefetch has something to overlap.
   int64_t rpw = (rows + 1023) / 1024;
-  if (rpw < kWaves) rpw = kWaves;
+  if (rpw < 2 * kWaves) rpw = 2 * kWaves;
   BwdPlan p;
   p.rows_per_wg = (int)rpw;
   p.nwg = (int)((rows + rpw - 1) / rpw);
@@ -338,7 +377,7 @@ int bwd_typed(const void *dy, int64_t dys, const void *x, int64_t xs, const void
   }
   int s = launch_status("pb_rmsnorm_bwd");
   if (s) return s;
-  hipLaunchKernelGGL((rmsnorm_dw_reduce<TW>), dim3((unsigned)((n + 63) / 64)), dim3(256), 0, st,
+  hipLaunchKernelGGL((rmsnorm_dw_reduce<TW>), dim3((unsigned)((n + 63) / 64)), dim3(1024), 0, st,
                      ws, static_cast<TW *>(dw), p.nwg, (int)n);
   return launch_status("pb_rmsnorm_bwd(dw)");
 }

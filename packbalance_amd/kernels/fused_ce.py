@@ -8,9 +8,11 @@ x's dtype and original shape and ``dw`` in W's dtype (fp32 accumulation).
 
 Forward: one MFMA GEMM kernel computes logits tiles in registers and keeps
 only per-token (max, sum-exp) partials and the target logit, then a combine
-kernel gives lse and the loss.  Backward streams the vocabulary in chunks of
-``VOCAB_CHUNK`` rows: a GEMM recomputes the chunk's logits and writes dlogits
-(bf16) directly, then two GEMMs accumulate dx and write the chunk's dW rows.
+kernel gives lse and the loss.  Backward streams the vocabulary in chunks
+(``vocab_chunk``: 8192 rows, or the whole vocabulary when one dlogits chunk
+of all tokens stays under ``CHUNK_BUDGET`` elements): a GEMM recomputes the
+chunk's logits and writes dlogits (bf16) directly, then two GEMMs accumulate
+dx and write the chunk's dW rows.
 Operands are bf16 with fp32 accumulation (fp32 inputs are rounded to bf16,
 as the reference's autocast GEMM does).  ``chunk_size`` (token rows per
 chunk in the reference) is accepted and validated; memory is bounded by the
@@ -68,10 +70,17 @@ def ce_rows(logits: torch.Tensor, targets: torch.Tensor, *, write_dlogits: bool,
 
 
 VOCAB_CHUNK = 8192
+CHUNK_BUDGET = 1 << 27  # dlogits elements per chunk (256 MB of bf16)
 
 
 def _round8(n: int) -> int:
     return (n + 7) // 8 * 8
+
+
+def vocab_chunk(n: int, v: int) -> int:
+    """Vocab rows per backward chunk: >= VOCAB_CHUNK, all of v if n*v fits the budget."""
+    fit = (CHUNK_BUDGET // max(1, n)) // 8 * 8
+    return min(_round8(v), max(VOCAB_CHUNK, fit))
 
 
 def _bf16_rows(t: torch.Tensor) -> torch.Tensor:
@@ -143,19 +152,17 @@ class _FusedLinearCE(torch.autograd.Function):
         dev = xb.device
         xt = _transpose_bf16(xb)  # [d8, n8]
         wt = _transpose_bf16(wb)  # [d8, v8]
-        vchunk = min(VOCAB_CHUNK, _round8(v))
-        dl = torch.empty((n, vchunk), dtype=torch.bfloat16, device=dev)
-        dlt = torch.empty((vchunk, xt.shape[1]), dtype=torch.bfloat16, device=dev)
-        dx_acc = torch.empty((n, d8), dtype=torch.float32, device=dev)
+        vchunk = vocab_chunk(n, v)
+        ws = torch.empty(N.lib().pb_lmhead_ce_bwd_workspace_bytes(n, v, d8, vchunk),
+                         dtype=torch.uint8, device=dev)
         dx = torch.empty((n, d8), dtype=ctx.x_dtype, device=dev)
         dw = torch.empty((v, d8), dtype=ctx.w_dtype, device=dev)
         go = grad_output.detach().to(torch.float32).reshape(1).contiguous()
         N.call("pb_lmhead_ce_bwd", xb.data_ptr(), xb.stride(0), wb.data_ptr(), wb.stride(0),
                xt.data_ptr(), xt.stride(0), wt.data_ptr(), wt.stride(0), n, v, d8,
                t.data_ptr(), ctx.ignore_index, ctx.z, lse.data_ptr(), go.data_ptr(), vchunk,
-               dl.data_ptr(), dl.stride(0), dlt.data_ptr(), dlt.stride(0), dx_acc.data_ptr(),
-               dx.data_ptr(), N.dtype_code(dx), dx.stride(0), dw.data_ptr(), N.dtype_code(dw),
-               dw.stride(0), N.stream_ptr(xb))
+               ws.data_ptr(), dx.data_ptr(), N.dtype_code(dx), dx.stride(0), dw.data_ptr(),
+               N.dtype_code(dw), dw.stride(0), N.stream_ptr(xb))
         d = ctx.d
         if d8 != d:
             dx, dw = dx[:, :d], dw[:, :d]

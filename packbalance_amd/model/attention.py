@@ -22,6 +22,8 @@ CPU tensors raise on the native path: there is no silent fallback.
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 import torch.nn.functional as F
 
@@ -124,13 +126,19 @@ def build_doc_block_mask(doc_ids: torch.Tensor, n_heads: int, block_size: int = 
 FWD, BWD_KV, BWD_Q = 0, 1, 2
 
 
+def attn_config(b: int, hq: int, hkv: int, s: int, d: int) -> dict:
+    """Tile sizes / workspace the kernels use for this shape (``pb_attn_config``)."""
+    out = (ctypes.c_int64 * 8)()
+    N.call("pb_attn_config", b, hq, hkv, s, d, out)
+    return {"tiles": {FWD: (out[0], out[1]), BWD_KV: (out[2], out[3]), BWD_Q: (out[4], out[5])},
+            "workspace": int(out[6]), "split": bool(out[7])}
+
+
 class _Plan:
     """Tile plan of a packed batch for one kernel (see ``pb_attn_plan``)."""
 
-    def __init__(self, doc: torch.Tensor, kernel: int, head_dim: int):
-        lib = N.lib()
-        self.q_tile = lib.pb_attn_tile(kernel, head_dim, 0)
-        self.kv_tile = lib.pb_attn_tile(kernel, head_dim, 1)
+    def __init__(self, doc: torch.Tensor, kernel: int, q_tile: int, kv_tile: int):
+        self.q_tile, self.kv_tile = q_tile, kv_tile
         by_kv = 1 if kernel == BWD_KV else 0
         b, s = doc.shape
         nq = -(-s // self.q_tile)
@@ -156,7 +164,7 @@ def _doc_2d(doc_ids: torch.Tensor, batch: int, seq_len: int) -> torch.Tensor:
     return d.contiguous()
 
 
-def _plans(doc: torch.Tensor, head_dim: int, block_mask) -> dict:
+def _plans(doc: torch.Tensor, hq: int, hkv: int, head_dim: int, block_mask) -> dict:
     """Plans for the three kernels; cached on a DocBlockMask built from the same doc_ids."""
     # The model passes the very doc_ids tensor the mask was built from; the
     # mask keeps it alive, so pointer identity is a sync-free cache key.
@@ -164,10 +172,13 @@ def _plans(doc: torch.Tensor, head_dim: int, block_mask) -> dict:
     if (isinstance(block_mask, DocBlockMask) and block_mask.doc_ids.shape == doc.shape
             and block_mask.doc_ids.data_ptr() == doc.data_ptr()):
         cache = block_mask._plans
-    key = ("plans", head_dim)
+    key = ("plans", hq, hkv, head_dim)
     if cache is not None and key in cache:
         return cache[key]
-    plans = {k: _Plan(doc, k, head_dim) for k in (FWD, BWD_KV, BWD_Q)}
+    b, s = doc.shape
+    cfg = attn_config(b, hq, hkv, s, head_dim)
+    plans = {k: _Plan(doc, k, *cfg["tiles"][k]) for k in (FWD, BWD_KV, BWD_Q)}
+    plans["workspace"] = cfg["workspace"]
     if cache is not None:
         cache[key] = plans
     return plans
@@ -201,11 +212,11 @@ class _DocAttention(torch.autograd.Function):
         dq = torch.empty((B, S, Hq, D), dtype=q.dtype, device=q.device).transpose(1, 2)
         dk = torch.empty((B, S, Hkv, D), dtype=k.dtype, device=k.device).transpose(1, 2)
         dv = torch.empty((B, S, Hkv, D), dtype=v.dtype, device=v.device).transpose(1, 2)
-        delta = torch.empty((B, Hq, S), dtype=torch.float32, device=q.device)
+        ws = torch.empty(ctx.plans["workspace"], dtype=torch.uint8, device=q.device)
         pq, pkv = ctx.plans[BWD_Q], ctx.plans[BWD_KV]
         N.call("pb_attn_bwd", N.BHSD.of(q), N.BHSD.of(k), N.BHSD.of(v), N.BHSD.of(out),
                N.BHSD.of(g), N.BHSD.of(dq), N.BHSD.of(dk), N.BHSD.of(dv), lse.data_ptr(),
-               delta.data_ptr(), doc.data_ptr(), doc.stride(0), pq.counts.data_ptr(),
+               ws.data_ptr(), doc.data_ptr(), doc.stride(0), pq.counts.data_ptr(),
                pq.lists.data_ptr(), pkv.counts.data_ptr(), pkv.lists.data_ptr(),
                B, Hq, Hkv, S, D, float(ctx.scale), N.PB_BF16, N.stream_ptr(q))
         return dq, dk, dv, None, None, None
@@ -235,7 +246,7 @@ def doc_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, doc_ids: to
     if D > 128:
         raise RuntimeError(f"head_dim {D} > 128 is not supported by the attention kernels")
     doc = _doc_2d(doc_ids, B, S)
-    plans = _plans(doc, D, block_mask)
+    plans = _plans(doc, Hq, k.shape[1], D, block_mask)
     sc = (1.0 / D ** 0.5) if scale is None else float(scale)
     dtype = q.dtype
     qb, kb, vb = (_bhsd(t.to(torch.bfloat16)) for t in (q, k, v))

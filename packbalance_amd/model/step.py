@@ -1,0 +1,94 @@
+"""The packed training step of the benchmark harness, eager or as one HIP graph.
+
+Semantics of the reference's ``profiling/bench_train.py:101-118``: for each
+pack of the step (one micro-batch each) build the document block mask, run
+the forward and ``(loss / step_tokens).backward()`` under bf16 autocast; then
+``clip_grad_norm_(1.0)`` and a fused AdamW step.
+
+``capture`` records that whole sequence once into a HIP graph on static
+device buffers (every hot-path op is capture-safe: no host synchronisation,
+device-resident grad scale, all workspaces from the caching allocator);
+``replay`` copies the next step's packs -- already resident in HBM -- into
+those buffers and replays it, so the ~5k kernel launches of a step cost one
+graph launch.  ``loss_sum`` and ``grad_norm`` hold the last step's summed
+loss and pre-clip gradient norm for checking replays against eager steps.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from packbalance_amd.model.attention import build_doc_block_mask
+from packbalance_amd.model.llama import LlamaForCausalLM
+
+
+class TrainStep:
+    def __init__(self, cfg, dev, packs_per_step: int = 4, seq_len: int | None = None,
+                 seed: int = 0, lr: float = 3e-4):
+        self.cfg, self.dev = cfg, dev
+        seq_len = seq_len or cfg.max_seq_len
+        torch.manual_seed(seed)
+        self.model = LlamaForCausalLM(cfg).to(dev)
+        self.model.train()
+        self.opt = torch.optim.AdamW(self.model.parameters(), lr=lr, betas=(0.9, 0.95),
+                                     weight_decay=0.1, fused=True, capturable=True)
+
+        def z():
+            return torch.zeros((1, seq_len), dtype=torch.int64, device=dev)
+
+        self.static = [dict(input_ids=z(), labels=z(), position_ids=z(), doc_ids=z())
+                       for _ in range(packs_per_step)]
+        self.step_tokens = torch.ones((), dtype=torch.float32, device=dev)
+        self.loss_sum = torch.zeros((), dtype=torch.float32, device=dev)
+        self.grad_norm = torch.zeros((), dtype=torch.float32, device=dev)
+        self.graph = None
+
+    def _body(self, batches, step_tokens) -> None:
+        self.loss_sum.zero_()
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            for b in batches:
+                bm = build_doc_block_mask(b["doc_ids"], self.cfg.n_heads)
+                loss = self.model(b["input_ids"], b["labels"], b["position_ids"], b["doc_ids"],
+                                  block_mask=bm)
+                (loss / step_tokens).backward()
+                self.loss_sum += loss.detach()
+        norm = torch.nn.utils.clip_grad_norm_(self.model.parameters(), 1.0)
+        self.grad_norm.copy_(norm)
+        self.opt.step()
+
+    @staticmethod
+    def _as_dicts(batch_list):
+        return [dict(input_ids=b.input_ids, labels=b.labels, position_ids=b.position_ids,
+                     doc_ids=b.doc_ids) for b in batch_list]
+
+    def eager(self, batch_list) -> None:
+        self.opt.zero_grad(set_to_none=True)
+        tokens = float(sum(b.useful_tokens for b in batch_list))
+        self._body(self._as_dicts(batch_list), tokens)
+
+    def _load(self, batch_list, tokens_dev) -> None:
+        for dst, b in zip(self.static, batch_list):
+            dst["input_ids"].copy_(b.input_ids)
+            dst["labels"].copy_(b.labels)
+            dst["position_ids"].copy_(b.position_ids)
+            dst["doc_ids"].copy_(b.doc_ids)
+        self.step_tokens.copy_(tokens_dev)
+
+    def capture(self, batch_list, tokens_dev, warmup_steps: int = 2) -> None:
+        """Warm up on a side stream (optimizer state, caches), then capture one step."""
+        self._load(batch_list, tokens_dev)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(warmup_steps):
+                self.opt.zero_grad(set_to_none=True)
+                self._body(self.static, self.step_tokens)
+        torch.cuda.current_stream().wait_stream(side)
+        self.opt.zero_grad(set_to_none=True)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self._body(self.static, self.step_tokens)
+
+    def replay(self, batch_list, tokens_dev) -> None:
+        self._load(batch_list, tokens_dev)
+        self.graph.replay()

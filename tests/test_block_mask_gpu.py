@@ -85,7 +85,7 @@ def test_build_doc_block_mask_rejects_batch(dev) -> None:
         build_doc_block_mask(torch.zeros(2, 64, dtype=torch.long, device=dev), 2)
 
 
-@pytest.mark.parametrize("q_tile,kv_tile,by_kv", [(128, 64, 0), (32, 128, 1), (64, 64, 0)])
+@pytest.mark.parametrize("q_tile,kv_tile,by_kv", [(128, 64, 0), (64, 128, 1), (64, 64, 0), (64, 64, 1)])
 def test_attention_plans_match_oracle(q_tile, kv_tile, by_kv, dev) -> None:
     """pb_attn_plan lists == the closed-form tile classes, ascending, FULL bit set."""
     from packbalance_amd import _native as N
