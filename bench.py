@@ -13,7 +13,10 @@ runs on):
   lmhead_ce  cfg4 fused LM-head CE fwd+bwd, 6*N*V*D FLOPs
   ce_rows    one cfg4 vocab chunk [16384 x 8192] bf16 through the row CE kernel
   rmsnorm / swiglu   cfg5 fwd and bwd, algorithmic bytes moved
-The ``roofline`` object is the attention forward kernel at cfg3 (MFMA-bound).
+The ``roofline`` object is the attention forward kernel at cfg3 (MFMA-bound):
+``achieved`` = 4*D*Hq*P FLOPs per launch / the launch's HIP-event duration;
+``traffic`` = HBM-side bytes per launch from the committed rocprofv3
+FETCH_SIZE / WRITE_SIZE summary (profiles/attention_cfg3_hbm_counters.txt).
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--skip-cpu] [--skip-kernels]
 """
@@ -47,6 +50,23 @@ def cpu_model_name() -> str:
     except OSError:
         pass
     return platform.processor() or "unknown"
+
+
+def counter_traffic(kernel_substr: str, summary: str = "attention_cfg3_hbm_counters.txt"):
+    """HBM-side bytes per launch of a kernel from a committed rocprofv3 counter summary.
+
+    The summary lists 2 x FETCH_SIZE + WRITE_SIZE per dispatch (the factor 2 is
+    the copy calibration written at its top); None when it is absent.
+    """
+    path = ROOT / "profiles" / summary
+    try:
+        for line in path.read_text().splitlines():
+            if line.startswith("#") or kernel_substr not in line:
+                continue
+            return float(line.split()[2]) * 1e9
+    except (OSError, ValueError, IndexError):
+        return None
+    return None
 
 
 # ---------------------------------------------------------------- timing
@@ -343,6 +363,19 @@ def norm_act_kernels(dev, iters: int, flush) -> dict:
     return out
 
 
+def copy_calibration(dev, iters: int) -> dict:
+    """A plain device copy of known size: the scale reference for HBM byte counters."""
+    import torch
+
+    n = 1 << 29  # 1 GiB of bf16
+    src = torch.randn(n // 2, device=dev).to(torch.bfloat16).repeat(2)
+    dst = torch.empty_like(src)
+    ms = events_ms(lambda: dst.copy_(src), iters)
+    nbytes = src.numel() * src.element_size()
+    return {"bytes_read": nbytes, "bytes_written": nbytes, "ms": ms,
+            "gbps": 2 * nbytes / ms / 1e6}
+
+
 # ---------------------------------------------------------------- main
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
@@ -354,7 +387,8 @@ def main() -> int:
     ap.add_argument("--skip-kernels", action="store_true")
     ap.add_argument("--eager", action="store_true",
                     help="run the training step eagerly instead of as one captured HIP graph")
-    ap.add_argument("--only", choices=["train", "attention", "lmhead_ce", "ce_rows", "norm_act"],
+    ap.add_argument("--only", choices=["train", "attention", "lmhead_ce", "ce_rows", "norm_act",
+                                       "copy"],
                     default=None, help="run one part only (for profiling)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -379,7 +413,8 @@ def main() -> int:
         fn = {"attention": lambda: attention_kernels(dev, args.kernel_iters),
               "lmhead_ce": lambda: lmhead_ce_kernels(dev, args.kernel_iters),
               "ce_rows": lambda: ce_rows_kernel(dev, args.kernel_iters, flush),
-              "norm_act": lambda: norm_act_kernels(dev, args.kernel_iters, flush)}[args.only]
+              "norm_act": lambda: norm_act_kernels(dev, args.kernel_iters, flush),
+              "copy": lambda: copy_calibration(dev, args.kernel_iters)}[args.only]
         print(json.dumps({args.only: fn()}), flush=True)
         return 0
 
@@ -398,9 +433,10 @@ def main() -> int:
         log("kernels: attention (cfg3)")
         kernels["attention"] = attention_kernels(dev, args.kernel_iters)
         a = kernels["attention"]
-        roofline = {"bound": "mfma", "kernel": "attn_fwd_kernel<128> (cfg3)",
+        roofline = {"bound": "mfma", "kernel": "attn_fwd_kernel<128, 4> (cfg3)",
                     "achieved": a["fwd_tflops"], "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                    "frac": a["fwd_tflops"] / PEAK_BF16_TFLOPS, "traffic": None}
+                    "frac": a["fwd_tflops"] / PEAK_BF16_TFLOPS,
+                    "traffic": counter_traffic("attn_fwd_kernel<128, 4>")}
         log("kernels: fused LM-head CE (cfg4)")
         kernels["lmhead_ce"] = lmhead_ce_kernels(dev, max(2, args.kernel_iters // 3))
         log("kernels: row CE chunk")
