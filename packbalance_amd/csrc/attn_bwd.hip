@@ -236,7 +236,7 @@ __global__ __launch_bounds__(256) void attn_bwd_reduce(BwdArgs a) {
 
 // ---------------------------------------------------------------- dQ
 template <int DP, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) void attn_bwd_dq(BwdArgs a) {
+__device__ __forceinline__ void dq_body(const BwdArgs &a) {
   constexpr int NT = 64 * WAVES;
   constexpr int BM = 32 * WAVES, BN = kKvStep;
   constexpr int KP = DP + 8;
@@ -249,10 +249,8 @@ __global__ __launch_bounds__(64 * WAVES) void attn_bwd_dq(BwdArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hh = lane >> 5, l32 = lane & 31;
-  const int bh = a.B * a.Hq;
-  const int qt = a.nqt_dq - 1 - (int)(blockIdx.x / bh);
-  const int rem = (int)(blockIdx.x % bh);
-  const int b = rem / a.Hq, h = rem - (rem / a.Hq) * a.Hq;
+  int qt, b, h;
+  decode_q_major((int)blockIdx.x, a.nqt_dq, a.B, a.Hq, a.Hkv, qt, b, h);
   const int hk = h / (a.Hq / a.Hkv);
   const bool vec = a.vec != 0;
   const int64_t *docb = a.doc + b * a.doc_sb;
@@ -357,6 +355,19 @@ __global__ __launch_bounds__(64 * WAVES) void attn_bwd_dq(BwdArgs a) {
     }
 }
 
+// Two entry points over one body: two waves per SIMD (so one wave's softmax
+// overlaps the other's MFMAs) wherever the registers fit without spilling.
+template <int DP, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+attn_bwd_dq(BwdArgs a) {
+  dq_body<DP, WAVES>(a);
+}
+
+template <int DP, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void attn_bwd_dq_wide(BwdArgs a) {
+  dq_body<DP, WAVES>(a);
+}
+
 View view_of(const pb_bhsd *t) {
   View v;
   v.p = static_cast<bf16_t *>(t->data);
@@ -432,7 +443,13 @@ extern "C" int pb_attn_bwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v,
   // dq first: it also writes delta = rowsum(dO * O), which dkdv reads.
   dim3 g_q((unsigned)(a.nqt_dq * b * hq));
   dim3 g_kv((unsigned)(a.nkt_kv * b * hkv * (cfg.split ? hq / hkv : 1)));
-#define PB_DQ(DP, W) hipLaunchKernelGGL((attn_bwd_dq<DP, W>), g_q, dim3(64 * W), 0, st, a)
+#define PB_DQ(DP, W)                                                                \
+  do {                                                                              \
+    if (DP == 128 && W == 2)                                                        \
+      hipLaunchKernelGGL((attn_bwd_dq_wide<DP, W>), g_q, dim3(64 * W), 0, st, a);   \
+    else                                                                            \
+      hipLaunchKernelGGL((attn_bwd_dq<DP, W>), g_q, dim3(64 * W), 0, st, a);        \
+  } while (0)
 #define PB_KV(DP, W, SP) hipLaunchKernelGGL((attn_bwd_dkdv<DP, W, SP>), g_kv, dim3(64 * W), 0, st, a)
 #define PB_BY_D(M, ...) \
   do { if (d <= 32) M(32, __VA_ARGS__); else if (d <= 64) M(64, __VA_ARGS__); else M(128, __VA_ARGS__); } while (0)

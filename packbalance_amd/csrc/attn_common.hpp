@@ -83,6 +83,32 @@ __device__ __forceinline__ bf16x8_t lds_col_frag(const bf16_t *tile, int pitch, 
   return *reinterpret_cast<bf16x8_t *>(&r);
 }
 
+// Grid decode of the query-major kernels (forward, dQ).  Workgroup i runs on
+// XCD i % 8 (each XCD has its own L2).  The G query heads that read one KV
+// head's K/V tiles are placed on the same XCD, 8 workgroup ids apart, so they
+// share those tiles in that XCD's L2; groups are ordered late query tile
+// first (the most causal work).  Within whole chunks of 8*G workgroups the
+// map is a bijection onto logical ids; the tail keeps the identity map.
+__device__ __forceinline__ void decode_q_major(int bid, int nqt, int B, int Hq, int Hkv, int &qt,
+                                               int &b, int &h) {
+  const int G = Hq / Hkv;
+  const int total = nqt * B * Hq;
+  const int chunk = 8 * G;
+  const int full = (total / chunk) * chunk;
+  int L = bid;  // logical id: group member fastest, then KV head, pack, late-first tile
+  if (bid < full) {
+    const int c = bid / chunk, r = bid - (bid / chunk) * chunk;
+    L = (c * 8 + (r & 7)) * G + (r >> 3);
+  }
+  const int g = L % G;
+  int t = L / G;
+  const int hk = t % Hkv;
+  t /= Hkv;
+  b = t % B;
+  qt = nqt - 1 - t / B;
+  h = hk * G + g;
+}
+
 // Packed plan entry: tile index << 1 | FULL flag.
 __device__ __forceinline__ int plan_tile(int e) { return e >> 1; }
 __device__ __forceinline__ bool plan_full(int e) { return e & 1; }

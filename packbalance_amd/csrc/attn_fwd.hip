@@ -44,7 +44,7 @@ struct FwdArgs {
 };
 
 template <int DP, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) void attn_fwd_kernel(FwdArgs a) {
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_fwd_kernel(FwdArgs a) {
   constexpr int NT = 64 * WAVES;
   constexpr int BM = 32 * WAVES, BN = kKvStep;
   constexpr int KP = DP + 8;  // K / V row pitch in LDS (elements)
@@ -60,11 +60,8 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd_kernel(FwdArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hh = lane >> 5, l32 = lane & 31;
 
-  // Late query tiles carry the most causal work: schedule them first.
-  const int bh = a.B * a.Hq;
-  const int qt = a.nqt - 1 - (int)(blockIdx.x / bh);
-  const int rem = (int)(blockIdx.x % bh);
-  const int b = rem / a.Hq, h = rem - (rem / a.Hq) * a.Hq;
+  int qt, b, h;
+  decode_q_major((int)blockIdx.x, a.nqt, a.B, a.Hq, a.Hkv, qt, b, h);
   const int hk = h / (a.Hq / a.Hkv);
   const int q0 = qt * BM;
 
