@@ -52,6 +52,10 @@ def cpu_model_name() -> str:
     return platform.processor() or "unknown"
 
 
+# The cfg3 forward launch: DMA-pipelined kernel, head dim 128, 32 query rows x 4 waves.
+FWD_KERNEL = "attn_fwd_pipe<128, 32, 4>"
+
+
 def counter_traffic(kernel_substr: str, summary: str = "attention_cfg3_hbm_counters.txt"):
     """HBM-side bytes per launch of a kernel from a committed rocprofv3 counter summary.
 
@@ -433,10 +437,10 @@ def main() -> int:
         log("kernels: attention (cfg3)")
         kernels["attention"] = attention_kernels(dev, args.kernel_iters)
         a = kernels["attention"]
-        roofline = {"bound": "mfma", "kernel": "attn_fwd_kernel<128, 4> (cfg3)",
+        roofline = {"bound": "mfma", "kernel": f"{FWD_KERNEL} (cfg3)",
                     "achieved": a["fwd_tflops"], "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                     "frac": a["fwd_tflops"] / PEAK_BF16_TFLOPS,
-                    "traffic": counter_traffic("attn_fwd_kernel<128, 4>")}
+                    "traffic": counter_traffic(FWD_KERNEL)}
         log("kernels: fused LM-head CE (cfg4)")
         kernels["lmhead_ce"] = lmhead_ce_kernels(dev, max(2, args.kernel_iters // 3))
         log("kernels: row CE chunk")

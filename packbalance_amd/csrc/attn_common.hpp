@@ -83,6 +83,123 @@ __device__ __forceinline__ bf16x8_t lds_col_frag(const bf16_t *tile, int pitch, 
   return *reinterpret_cast<bf16x8_t *>(&r);
 }
 
+// 64-row K / V / Q / dO tiles in LDS without padding.  Rows are packed into
+// 256-byte lines (1, 2 or 4 rows per line for head dims 128, 64, 32) and the
+// 16-byte chunks of a line are XOR-permuted by a function of the line index.
+// Measured with SQ_LDS_BANK_CONFLICT on gfx950, this layout is conflict-free
+// both for ds_read_b128 row fragments (32 consecutive rows, one chunk each)
+// and for the ds_read_b64_tr_b16 column fragments of lds_col_frag (8 rows x 4
+// chunks per wave); a padded row pitch serves only one of the two (pitch
+// DP+8 costs 2.7 conflict cycles per transposing read).
+template <int DP>
+struct SwzTile {
+  static constexpr int CPR = DP / 8;   // 16-byte chunks per row
+  static constexpr int RPL = 16 / CPR;  // rows per 256-byte line
+  static constexpr int BYTES = 64 * DP * 2;
+  static_assert(DP == 32 || DP == 64 || DP == 128, "head dim tile");
+  __device__ static __forceinline__ int xmask(int line) {
+    if constexpr (CPR == 16) return ((line & 3) << 2) | ((line >> 2) & 3);
+    else if constexpr (CPR == 8) return ((line & 1) << 2) | ((line >> 1) & 3);
+    else return line & 3;
+  }
+  // Byte offset of element `col` (a multiple of 4) of row r.
+  __device__ static __forceinline__ int off(int r, int col) {
+    const int line = r / RPL;
+    return ((line * 16 + (r % RPL) * CPR + ((col >> 3) ^ xmask(line))) << 4) + ((col & 7) << 1);
+  }
+  // Row r and chunk c (8 elements) held by LDS chunk p of the tile.
+  __device__ static __forceinline__ void at(int p, int &r, int &c) {
+    const int line = p >> 4, slot = p & 15;
+    r = line * RPL + slot / CPR;
+    c = (slot % CPR) ^ xmask(line);
+  }
+};
+
+// Row fragment (8 consecutive columns col..col+7 of row r) of a swizzled tile.
+template <int DP>
+__device__ __forceinline__ bf16x8_t swz_row_frag(const char *tile, int r, int col) {
+  return *reinterpret_cast<const bf16x8_t *>(tile + SwzTile<DP>::off(r, col));
+}
+
+// lds_col_frag on a swizzled tile: lane l gets column col0 + l%32 at k slots
+// k0 + pi(h, s).
+template <int DP>
+__device__ __forceinline__ bf16x8_t swz_col_frag(const char *tile, int k0, int col0, int lane) {
+  const int j = lane & 15, g = lane >> 4, h = lane >> 5;
+  const int col = col0 + 16 * (g & 1) + 4 * (j & 3);
+  const int row = k0 + 4 * h + (j >> 2);
+  const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_i16x4_t *)(tile + SwzTile<DP>::off(row, col)));
+  const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_i16x4_t *)(tile + SwzTile<DP>::off(row + 8, col)));
+  typedef short i16x8_t __attribute__((ext_vector_type(8)));
+  i16x8_t r = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return *reinterpret_cast<bf16x8_t *>(&r);
+}
+
+// Copy ROWS rows (kv0.., DP columns of a [rows][ss] bf16 view at byte address
+// `base`) into a swizzled LDS tile with global_load_lds_dwordx4: lane i of a
+// wave-level instruction writes LDS bytes [16i, 16i+16) of its 1 KiB slice,
+// so each lane fetches the global chunk that the swizzle puts there.
+// `off[i]` = byte offset of that chunk within the tile (precomputed per
+// thread).  The caller guarantees kv0 + ROWS <= sequence length.  Every
+// thread issues exactly NDMA instructions; completion is tracked by vmcnt.
+template <int DP, int ROWS, int NT>
+struct TileDma {
+  static constexpr int NDMA = ROWS * DP * 2 / 16 / NT;
+  static_assert(NDMA >= 1 && ROWS * DP * 2 / 16 == NDMA * NT, "tile/thread mismatch");
+  __device__ static __forceinline__ void offsets(int64_t ss, int wave, int lane, uint32_t *off) {
+#pragma unroll
+    for (int i = 0; i < NDMA; ++i) {
+      int r, c;
+      SwzTile<DP>::at((i * (NT / 64) + wave) * 64 + lane, r, c);
+      off[i] = (uint32_t)((r * ss + c * 8) * 2);
+    }
+  }
+  __device__ static __forceinline__ void copy(const char *base, int64_t ss, const uint32_t *off,
+                                              int kv0, char *dst, int wave) {
+    const char *tb = base + (int64_t)kv0 * ss * 2;
+    constexpr int W = NT / 64;
+#pragma unroll
+    for (int i = 0; i < NDMA; ++i)
+      __builtin_amdgcn_global_load_lds(
+          tb + off[i], (__attribute__((address_space(3))) void *)(dst + (i * W + wave) * 1024), 16,
+          0, 0);
+  }
+};
+
+// s_waitcnt vmcnt(N) with expcnt / lgkmcnt left alone: all but the N most
+// recent vector-memory operations (loads, LDS DMA) of this wave have landed.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier without __syncthreads' memory fence: the fence would
+// wait for every outstanding vector-memory operation (vmcnt(0)), including
+// LDS DMA deliberately left in flight.  The caller waits for the DMA it needs
+// (wait_vmcnt) first; the empty asm statements keep the compiler from moving
+// memory accesses across the barrier.
+__device__ __forceinline__ void block_sync_nofence() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Exchange with lane ^ 32 without LDS (v_permlane32_swap): returns
+// f(x, x of the partner lane) for a commutative f.
+__device__ __forceinline__ float xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Grid decode of the query-major kernels (forward, dQ).  Workgroup i runs on
 // XCD i % 8 (each XCD has its own L2).  The G query heads that read one KV
 // head's K/V tiles are placed on the same XCD, 8 workgroup ids apart, so they
@@ -157,8 +274,9 @@ inline AttnConfig attn_config(int64_t b, int64_t hq, int64_t hkv, int64_t s, int
   const int64_t kFill = 512;  // two workgroups per CU on 256 CUs
   auto tiles = [&](int rows) { return (s + rows - 1) / rows; };
   AttnConfig c;
-  c.fwd_waves = b * hq * tiles(128) >= kFill ? 4 : 2;
-  c.dq_waves = c.fwd_waves;
+  const bool big_q = b * hq * tiles(128) >= kFill;
+  c.fwd_waves = big_q ? 4 : 2;
+  c.dq_waves = big_q ? 4 : 2;
   c.kv_waves = b * hkv * tiles(128) >= kFill ? 4 : 2;
   c.split = (c.kv_waves == 2 && b * hkv * tiles(64) < kFill && hq > hkv) ? 1 : 0;
   return c;

@@ -15,10 +15,17 @@
 // one exchange with lane^32, and the O^T accumulator of a lane belongs to a
 // single query (one rescale factor per lane).  P^T leaves the accumulators as
 // the B operand of O^T += V^T P^T directly (see attn_common.hpp for the k-slot
-// permutation), so P never touches LDS.  K and V are staged row-major in LDS;
-// V^T fragments come from the transposing LDS load ds_read_b64_tr_b16.  The
-// next tile's K/V are prefetched into registers while the current one is
-// computed.
+// permutation), so P never touches LDS; V^T fragments come from the
+// transposing LDS load ds_read_b64_tr_b16.
+//
+// Two kernels share this scheme: attn_fwd_pipe (16-byte aligned views, head
+// dim 64 or 128, sequence a multiple of 64: DMA-fed swizzled LDS rings and a
+// software-pipelined body, described below) and attn_fwd_generic (everything
+// else: K/V staged through registers into padded LDS tiles, element-wise
+// loads where 16-byte access is not allowed).
+#include <algorithm>
+#include <type_traits>
+
 #include "attn_common.hpp"
 
 namespace pb {
@@ -43,8 +50,10 @@ struct FwdArgs {
   int vec;    // 16-byte global access allowed
 };
 
+// Generic path: any head dim <= 128, any strides / alignment (element-wise
+// loads where 16-byte access is not allowed), K/V staged through registers.
 template <int DP, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_fwd_kernel(FwdArgs a) {
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_fwd_generic(FwdArgs a) {
   constexpr int NT = 64 * WAVES;
   constexpr int BM = 32 * WAVES, BN = kKvStep;
   constexpr int KP = DP + 8;  // K / V row pitch in LDS (elements)
@@ -210,6 +219,383 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   }
 }
 
+// Pipelined path (16-byte aligned views and documents, D == DP in {64, 128},
+// sequence length a multiple of 64).
+//
+// A wave owns MQ query rows (NQB = MQ/32 column blocks of S^T; each K / V
+// fragment read from LDS feeds NQB MFMAs).  The launch uses MQ = 32, two
+// waves per SIMD: MQ = 64 halves the LDS reads per MFMA but needs ~400
+// registers, one wave per SIMD and AGPR<->VGPR copies, and measured slower
+// (2.34 vs 1.94 ms on 8 x 8192-token packs, 32/8 heads, D 128).
+// The KV tiles of the plan are walked as 32-row sub-tiles u.  K and V
+// sub-tiles are copied global -> LDS by DMA (global_load_lds_dwordx4) into
+// the swizzled layout, through 3-slot rings (slot = u % 3, compile-time in the
+// 3x unrolled loop), one barrier per sub-tile.  Body u issues the DMA of
+// K(u+3) and V(u+2), then runs an explicit software pipeline: for each of the
+// DP/16 head-dim steps of S(u+1) = K(u+1) Q^T it issues that step's MFMAs and
+// a fixed slice of the online softmax of S(u) (max, then exponentials), in
+// that order (sched_barrier fences keep the compiler from regrouping them),
+// so the VALU work runs under the MFMAs.  O^T += V(u)^T P(u)^T follows, with
+// the V fragments already read during the softmax steps.  The body finally
+// waits only for the DMA issued one body earlier.  The running max moves
+// only when a sub-tile's max exceeds it by more than kTau (log2 units), so
+// the O rescale is a rare wave-uniform branch and P stays below 2^kTau.
+template <int DP, int MQ, int WAVES>
+__global__ __launch_bounds__(64 * WAVES)
+__attribute__((amdgpu_waves_per_eu(MQ == 64 ? 1 : 2, MQ == 64 ? 1 : 2)))
+void attn_fwd_pipe(FwdArgs a) {
+  constexpr int NT = 64 * WAVES, NQB = MQ / 32, BM = MQ * WAVES;
+  constexpr int NDK = DP / 16, NDB = DP / 32;
+  constexpr int HB = 32 * DP * 2;  // bytes of one 32-row sub-tile
+  using Dma = TileDma<DP, 32, NT>;
+  constexpr int NDMA = Dma::NDMA;
+  constexpr float kTau = 8.0f;
+  // Softmax schedule over the NDK steps: step 0 row max, step 1 lane-pair
+  // max and new running max, steps 2.. the 8*NQB exponential pairs.
+  constexpr int NPAIR = 8 * NQB;
+  constexpr int PPS = (NPAIR + NDK - 3) / (NDK - 2);
+  constexpr int NVF = 2 * NDB;                    // V fragments per sub-tile
+  constexpr int VPS = (NVF + NDK / 2 - 1) / (NDK / 2);  // read in steps NDK/2..
+  static_assert(NDK >= 4, "head dim");
+  // Ring slots are separate LDS objects so that the compiler can tell a
+  // fragment read of one slot from the DMA still in flight into another (it
+  // would otherwise wait for all outstanding DMA before every read).
+  __shared__ __align__(16) char ks0[HB], ks1[HB], ks2[HB];
+  __shared__ __align__(16) char vs0[HB], vs1[HB], vs2[HB];
+  __shared__ __align__(16) int64_t kd0[32], kd1[32], kd2[32];
+  auto kslot = [&](auto Rc) -> char * {
+    if constexpr (decltype(Rc)::value == 0) return ks0;
+    else if constexpr (decltype(Rc)::value == 1) return ks1;
+    else return ks2;
+  };
+  auto vslot = [&](auto Rc) -> char * {
+    if constexpr (decltype(Rc)::value == 0) return vs0;
+    else if constexpr (decltype(Rc)::value == 1) return vs1;
+    else return vs2;
+  };
+  auto dslot = [&](auto Rc) -> int64_t * {
+    if constexpr (decltype(Rc)::value == 0) return kd0;
+    else if constexpr (decltype(Rc)::value == 1) return kd1;
+    else return kd2;
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hh = lane >> 5, l32 = lane & 31;
+  int qt, b, h;
+  decode_q_major((int)blockIdx.x, a.nqt, a.B, a.Hq, a.Hkv, qt, b, h);
+  const int hk = h / (a.Hq / a.Hkv);
+  const int S = a.S;
+  const char *Kb = reinterpret_cast<const char *>(a.k + b * a.k_sb + hk * a.k_sh);
+  const char *Vb = reinterpret_cast<const char *>(a.v + b * a.v_sb + hk * a.v_sh);
+  const int64_t *docb = a.doc + b * a.doc_sb;
+  const float sl2 = a.sl2;
+
+  uint32_t koff[NDMA], voff[NDMA];
+  Dma::offsets(a.k_ss, wave, lane, koff);
+  Dma::offsets(a.v_ss, wave, lane, voff);
+  // Per-lane byte offsets of the fragments within a sub-tile: K row
+  // fragments (row l32, columns 16dk + 8hh) and the two transposing reads of
+  // a V column fragment (rows 4hh + j/4 and +8, column 32db + ...); rows
+  // 16..31 repeat the swizzle of rows 0..15 at +16 * DP * 2 bytes.  Kept in
+  // registers for the whole loop (the empty asm stops rematerialisation).
+  int koffs[NDK], voffs[NDB][2];
+  {
+    const int j = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int dk = 0; dk < NDK; ++dk) {
+      koffs[dk] = SwzTile<DP>::off(l32, 16 * dk + 8 * hh);
+      asm volatile("" : "+v"(koffs[dk]));
+    }
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const int col = 32 * db + 16 * (g & 1) + 4 * (j & 3);
+      const int row = 4 * hh + (j >> 2);
+      voffs[db][0] = SwzTile<DP>::off(row, col);
+      voffs[db][1] = SwzTile<DP>::off(row + 8, col);
+      asm volatile("" : "+v"(voffs[db][0]), "+v"(voffs[db][1]));
+    }
+  }
+  auto kfrag = [&](const char *kt, int dk) {
+    return *reinterpret_cast<const bf16x8_t *>(kt + koffs[dk]);
+  };
+  auto vfrag_of = [&](int f, const char *vt) {  // f = kk * NDB + db
+    const char *base = vt + (f / NDB) * 16 * DP * 2;
+    const int db = f % NDB;
+    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(base + voffs[db][0]));
+    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(base + voffs[db][1]));
+    typedef short i16x8_t __attribute__((ext_vector_type(8)));
+    i16x8_t r = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return *reinterpret_cast<bf16x8_t *>(&r);
+  };
+
+  // This lane's query rows (one per 32-column block), documents, Q fragments.
+  int qi[NQB];
+  bool qv[NQB];
+  int64_t qdoc[NQB];
+  bf16x8_t qf[NQB][NDK];
+#pragma unroll
+  for (int qb = 0; qb < NQB; ++qb) {
+    qi[qb] = qt * BM + wave * MQ + qb * 32 + l32;
+    qv[qb] = qi[qb] < S;
+    const int qr = qv[qb] ? qi[qb] : S - 1;
+    qdoc[qb] = docb[qr];
+    const bf16_t *qrow = a.q + b * a.q_sb + h * a.q_sh + (int64_t)qr * a.q_ss;
+#pragma unroll
+    for (int dk = 0; dk < NDK; ++dk)
+      qf[qb][dk] = *reinterpret_cast<const bf16x8_t *>(qrow + 16 * dk + 8 * hh);
+  }
+
+  f32x16_t oacc[NQB][NDB];
+  float m_run[NQB], l_run[NQB];
+#pragma unroll
+  for (int qb = 0; qb < NQB; ++qb) {
+    m_run[qb] = -INFINITY;
+    l_run[qb] = 0.f;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) oacc[qb][db] = zero16();
+  }
+
+  const int cnt = a.cnt[b * a.nqt + qt];
+  const int U = 2 * cnt;  // 32-row sub-tiles
+  const int32_t *lst = a.list + ((int64_t)b * a.nqt + qt) * a.nkt;
+  // Plan entry of sub-tile u (clamped to the last one).  Loaded one body
+  // ahead and ahead of that body's DMA, so waiting for it never waits for
+  // DMA (vmcnt counts in issue order).
+  auto entry = [&](int u) { return lst[(u < U ? u : U - 1) >> 1]; };
+  auto row0 = [&](int e, int u) { return plan_tile(e) * kKvStep + 32 * (u & 1); };
+
+  // Element mask of a PARTIAL sub-tile: same document and kv <= q.
+  auto mask = [&](f32x16_t (&sv)[NQB], int kv0, const int64_t *kd) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int kr = 8 * (j >> 2) + 4 * hh + (j & 3);
+      const int64_t dkv = kd[kr];
+#pragma unroll
+      for (int qb = 0; qb < NQB; ++qb) {
+        const bool ok = qv[qb] && kv0 + kr <= qi[qb] && dkv == qdoc[qb];
+        sv[qb][j] = ok ? sv[qb][j] : -INFINITY;
+      }
+    }
+  };
+
+  // Softmax state of the sub-tile being exponentiated.
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  float mx[NQB], m_new[NQB], m_use[NQB], lt[NQB];
+  bool need = false;
+  // Slice `step` of the online softmax of S(u) (see the schedule above).
+  // Each step's results pass through an empty volatile asm, so they are
+  // computed inside the step (between the MFMAs it is paired with) instead of
+  // being sunk towards their first use.
+  auto softmax_step = [&](int step, const f32x16_t (&sv)[NQB], bf16x8_t (&pf)[NQB][2]) {
+    if (step == 0) {
+#pragma unroll
+      for (int qb = 0; qb < NQB; ++qb) {
+        float m0 = sv[qb][0];
+#pragma unroll
+        for (int j = 1; j < 16; ++j) m0 = fmaxf(m0, sv[qb][j]);
+        mx[qb] = m0;
+        lt[qb] = 0.f;
+        asm volatile("" ::"v"(mx[qb]));
+      }
+    } else if (step == 1) {
+      need = false;
+#pragma unroll
+      for (int qb = 0; qb < NQB; ++qb) {
+        const float m1 = xor32_max(mx[qb]) * sl2;
+        const bool nq = m1 > m_run[qb] + kTau;
+        need |= nq;
+        m_new[qb] = nq ? m1 : m_run[qb];
+        m_use[qb] = m_new[qb] == -INFINITY ? 0.f : m_new[qb];
+        asm volatile("" ::"v"(m_use[qb]), "v"(m_new[qb]));
+      }
+    } else {
+#pragma unroll
+      for (int p = (step - 2) * PPS; p < (step - 1) * PPS && p < NPAIR; ++p) {
+        const int qb = p / 8, j = 2 * (p % 8);
+        // The row sum takes the fp32 values (as the reference's softmax does);
+        // only the PV operand is rounded to bf16.
+        const float p0 = fast_exp2(fmaf(sv[qb][j], sl2, -m_use[qb]));
+        const float p1 = fast_exp2(fmaf(sv[qb][j + 1], sl2, -m_use[qb]));
+        lt[qb] += p0 + p1;
+        bf16x2_t pp;
+        pp[0] = (bf16_t)p0;
+        pp[1] = (bf16_t)p1;
+        asm volatile("" ::"v"(*reinterpret_cast<uint32_t *>(&pp)), "v"(lt[qb]));
+        pf[qb][j >> 3][j & 7] = pp[0];
+        pf[qb][j >> 3][(j & 7) + 1] = pp[1];
+      }
+    }
+  };
+  // Rare rescale of O when some lane moved its running max, then the sums.
+  auto softmax_commit = [&]() {
+    if (__builtin_expect(__builtin_amdgcn_ballot_w64(need) != 0, 0)) {
+#pragma unroll
+      for (int qb = 0; qb < NQB; ++qb) {
+        // Lanes whose max did not move keep alpha = 1 (their max may still be
+        // -inf, where the difference would be NaN).
+        const float alpha = m_new[qb] == m_run[qb] ? 1.f : fast_exp2(m_run[qb] - m_new[qb]);
+        l_run[qb] *= alpha;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) oacc[qb][db] *= alpha;
+      }
+    }
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) {
+      m_run[qb] = m_new[qb];
+      l_run[qb] += lt[qb];
+    }
+  };
+  auto pv_step = [&](int f, const bf16x8_t &vf, const bf16x8_t (&pf)[NQB][2]) {
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb)
+      oacc[qb][f % NDB] = mfma32(vf, pf[qb][f / NDB], oacc[qb][f % NDB]);
+  };
+
+  // kdoc of sub-tile rows kv0..kv0+31 into a ring slot: one DMA instruction
+  // by 16 lanes of wave 0 (issued for every sub-tile, read for PARTIAL ones).
+  auto load_kdoc = [&](int kv0, int64_t *dst) {
+    if (wave == 0 && lane < 16)
+      __builtin_amdgcn_global_load_lds(docb + kv0 + 2 * lane,
+                                       (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+  };
+
+  f32x16_t sc[NQB];
+  if (U > 0) {
+    // Prologue: K(0..2), V(0..1) and their documents, then S(0).  U >= 2.
+    int ew[4];  // entries of sub-tiles u+1 .. u+4 for body u (see below)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ew[i] = entry(i + 1);
+    auto prefetch = [&](auto Rc, int u) {
+      const int e = entry(u);
+      load_kdoc(row0(e, u), dslot(Rc));
+      Dma::copy(Kb, a.k_ss, koff, row0(e, u), kslot(Rc), wave);
+      if (decltype(Rc)::value < 2) Dma::copy(Vb, a.v_ss, voff, row0(e, u), vslot(Rc), wave);
+    };
+    prefetch(I0(), 0);
+    prefetch(I1(), 1);
+    prefetch(I2(), 2);  // repeats sub-tile 1 when U == 2
+    wait_vmcnt<0>();
+    __syncthreads();
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) sc[qb] = zero16();
+#pragma unroll
+    for (int dk = 0; dk < NDK; ++dk) {
+      const bf16x8_t kf = kfrag(ks0, dk);
+#pragma unroll
+      for (int qb = 0; qb < NQB; ++qb) sc[qb] = mfma32(kf, qf[qb][dk], sc[qb]);
+    }
+    {
+      const int e = entry(0);
+      if (!plan_full(e)) mask(sc, row0(e, 0), kd0);
+    }
+    __syncthreads();  // K slot 0 is refilled by body 0
+
+    // Body u (u + 1 < U), ring slot R = u % 3.
+    // Every body issues the same DMA (past the last sub-tile, entry() repeats
+    // it into a slot nobody reads any more), so the number of operations in
+    // flight -- and the vmcnt to wait for -- is the same in every body.
+    auto body = [&](auto Rc, int u) {
+      constexpr int R = decltype(Rc)::value;
+      constexpr int R1 = (R + 1) % 3, R2 = (R + 2) % 3;
+      const int e1 = __builtin_amdgcn_readfirstlane(ew[0]);
+      const int e2 = __builtin_amdgcn_readfirstlane(ew[1]);
+      const int e3 = __builtin_amdgcn_readfirstlane(ew[2]);
+      const int e4 = entry(u + 5);  // for body u + 1, issued before this body's DMA
+      __builtin_amdgcn_sched_barrier(0);
+      using IR = std::integral_constant<int, R>;
+      using IR1 = std::integral_constant<int, R1>;
+      using IR2 = std::integral_constant<int, R2>;
+      load_kdoc(row0(e3, u + 3), dslot(IR()));
+      Dma::copy(Kb, a.k_ss, koff, row0(e3, u + 3), kslot(IR()), wave);
+      Dma::copy(Vb, a.v_ss, voff, row0(e2, u + 2), vslot(IR2()), wave);
+      bf16x8_t kf[NDK], vf[NVF], pf[NQB][2];
+#pragma unroll
+      for (int dk = 0; dk < NDK; ++dk) kf[dk] = kfrag(kslot(IR1()), dk);
+      f32x16_t sn[NQB];
+#pragma unroll
+      for (int qb = 0; qb < NQB; ++qb) sn[qb] = zero16();
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int dk = 0; dk < NDK; ++dk) {
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) sn[qb] = mfma32(kf[dk], qf[qb][dk], sn[qb]);
+        softmax_step(dk, sc, pf);
+        if (dk >= NDK / 2) {
+#pragma unroll
+          for (int f = (dk - NDK / 2) * VPS; f < (dk - NDK / 2 + 1) * VPS && f < NVF; ++f)
+            vf[f] = vfrag_of(f, vslot(IR()));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      softmax_commit();
+      // O^T += V(u)^T P(u)^T, with S(u+1) moved into sc alongside.
+#pragma unroll
+      for (int f = 0; f < NVF; ++f) {
+        pv_step(f, vf[f], pf);
+        if (f < NQB) sc[f] = sn[f];
+      }
+      if (!plan_full(e1)) mask(sc, row0(e1, u + 1), dslot(IR1()));
+      // The DMA just issued may stay in flight; everything older (the previous
+      // body's DMA, this body's entry load and document DMA) must land.
+      wait_vmcnt<2 * NDMA>();
+      block_sync_nofence();
+      ew[0] = ew[1];
+      ew[1] = ew[2];
+      ew[2] = ew[3];
+      ew[3] = e4;
+    };
+    int u = 0;
+    for (; u + 3 < U; u += 3) {
+      body(I0(), u);
+      body(I1(), u + 1);
+      body(I2(), u + 2);
+    }
+    if (u + 1 < U) {
+      body(I0(), u);
+      ++u;
+    }
+    if (u + 1 < U) {
+      body(I1(), u);
+      ++u;
+    }
+    wait_vmcnt<0>();  // the repeated DMA of the last bodies
+    // Last sub-tile: no S(u+1); its V sits in slot u % 3.
+    const int rl = u % 3;
+    const char *vt = rl == 0 ? vs0 : rl == 1 ? vs1 : vs2;
+    bf16x8_t pf[NQB][2];
+#pragma unroll
+    for (int step = 0; step < NDK; ++step) softmax_step(step, sc, pf);
+    softmax_commit();
+#pragma unroll
+    for (int f = 0; f < NVF; ++f) pv_step(f, vfrag_of(f, vt), pf);
+  }
+
+#pragma unroll
+  for (int qb = 0; qb < NQB; ++qb) {
+    const float lsum = xor32_sum(l_run[qb]);
+    const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
+    if (!qv[qb]) continue;
+    bf16_t *orow = a.o + b * a.o_sb + (int64_t)qi[qb] * a.o_ss + h * a.o_sh;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq) {
+        typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+        bf16x4_t o4;
+#pragma unroll
+        for (int x = 0; x < 4; ++x) o4[x] = (bf16_t)(oacc[qb][db][4 * jq + x] * inv);
+        *reinterpret_cast<bf16x4_t *>(orow + 32 * db + 8 * jq + 4 * hh) = o4;
+      }
+    if (hh == 0)
+      a.lse[((int64_t)b * a.Hq + h) * S + qi[qb]] =
+          lsum > 0.f ? m_run[qb] + fast_log2(lsum) : -INFINITY;
+  }
+}
+
 }  // namespace attn
 }  // namespace pb
 
@@ -250,12 +636,28 @@ extern "C" int pb_attn_fwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v,
   a.vec = views_vectorizable(d, {q, k, v, out});
   dim3 grid((unsigned)(a.nqt * b * hq));
   hipStream_t st = as_stream(stream);
-#define PB_FWD(DP, W) hipLaunchKernelGGL((attn_fwd_kernel<DP, W>), grid, dim3(64 * W), 0, st, a)
-  if (cfg.fwd_waves == 4) {
-    if (d <= 32) PB_FWD(32, 4); else if (d <= 64) PB_FWD(64, 4); else PB_FWD(128, 4);
+  // DMA tile offsets are 32-bit: 64 rows of K / V must span < 2 GiB.
+  const bool pipe = a.vec && (d == 64 || d == 128) && s % 64 == 0 &&
+                    (reinterpret_cast<uintptr_t>(doc_ids) & 15) == 0 && doc_stride % 2 == 0 &&
+                    64 * std::max(k->stride_s, v->stride_s) < (1LL << 30);
+  if (pipe) {
+#define PB_PIPE(DP, W) hipLaunchKernelGGL((attn_fwd_pipe<DP, 32, W>), grid, dim3(64 * W), 0, st, a)
+    if (cfg.fwd_waves == 4) {
+      if (d == 128) PB_PIPE(128, 4); else PB_PIPE(64, 4);
+    } else {
+      if (d == 128) PB_PIPE(128, 2); else PB_PIPE(64, 2);
+    }
+#undef PB_PIPE
   } else {
-    if (d <= 32) PB_FWD(32, 2); else if (d <= 64) PB_FWD(64, 2); else PB_FWD(128, 2);
-  }
+    // Generic kernel: 32 query rows per wave, same query tile as the plan.
+    const int w = cfg.fwd_q_tile() / 32;
+#define PB_FWD(DP, W) hipLaunchKernelGGL((attn_fwd_generic<DP, W>), grid, dim3(64 * W), 0, st, a)
+    if (w == 4) {
+      if (d <= 32) PB_FWD(32, 4); else if (d <= 64) PB_FWD(64, 4); else PB_FWD(128, 4);
+    } else {
+      if (d <= 32) PB_FWD(32, 2); else if (d <= 64) PB_FWD(64, 2); else PB_FWD(128, 2);
+    }
 #undef PB_FWD
+  }
   return launch_status("pb_attn_fwd");
 }

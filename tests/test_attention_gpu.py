@@ -89,6 +89,8 @@ def test_reference_flex_test_case(dev) -> None:
         (1, 8, 8, 1000, 128, [1000]),  # one dense doc, S not a tile multiple
         (1, 6, 2, 200, 128, [1] * 50 + [150]),  # single-token documents
         (3, 4, 4, 130, 100, [64, 66]),  # head dim not a multiple of 16
+        (1, 8, 2, 1024, 128, [300, 1, 400, -323]),  # pipelined path, 32 query rows per wave
+        (2, 16, 4, 2048, 64, "cfg2"),  # pipelined path, 64 query rows per wave, D 64
     ],
 )
 def test_attention_matches_oracle(B, Hq, Hkv, S, D, docs, dev) -> None:
@@ -104,14 +106,22 @@ def test_attention_matches_oracle(B, Hq, Hkv, S, D, docs, dev) -> None:
 
 
 def test_attention_contiguous_layout_and_scale(dev) -> None:
+    """Contiguous [B, H, S, D] views and a non-default scale (0.3 = 2.4x 1/sqrt(64)).
+
+    The gradients grow with the scale (dQ, dK carry it as a factor and P gets
+    sharper), and their error is dominated by the bf16 rounding of O entering
+    D = rowsum(dO * O) -- present in any bf16-output implementation -- so the
+    absolute gradient tolerance is scaled by scale * sqrt(D) = 2.4 here.
+    """
     q, k, v, do = _inputs(1, 4, 2, 192, 64, dev, model_layout=False)
     doc = W.doc_ids_from_lengths([[70, 122]], 192).to(dev)
     out, dq, dk, dv = _run(q, k, v, do, doc, scale=0.3)
     ref = OA.attention(q, k, v, doc.cpu(), do, scale=0.3)
     _close(out, ref["out"], "out")
-    _close(dq, ref["dq"], "dq")
-    _close(dk, ref["dk"], "dk")
-    _close(dv, ref["dv"], "dv")
+    gtol = TOL * 0.3 * math.sqrt(64)
+    for got, name in ((dq, "dq"), (dk, "dk"), (dv, "dv")):
+        torch.testing.assert_close(got.detach().float().cpu(), ref[name].float(), atol=gtol,
+                                   rtol=TOL, msg=lambda m, n=name: f"{n}: {m}")
 
 
 def test_attention_noncontiguous_documents(dev) -> None:
@@ -120,6 +130,14 @@ def test_attention_noncontiguous_documents(dev) -> None:
     ids = torch.tensor([i % 3 for i in range(S)], device=dev)[None]
     q, k, v, do = _inputs(1, 2, 1, S, 32, dev, seed=7)
     _check(q, k, v, do, ids, "alternating docs")
+
+
+def test_attention_noncontiguous_documents_pipelined(dev) -> None:
+    """Same, at a shape the DMA-pipelined forward takes (S % 64 == 0, D 64)."""
+    S = 256
+    ids = torch.tensor([(i // 7) % 3 for i in range(S)], device=dev)[None]
+    q, k, v, do = _inputs(1, 4, 2, S, 64, dev, seed=9)
+    _check(q, k, v, do, ids, "alternating docs, pipelined")
 
 
 def test_attention_forward_dispatch_and_eager_rows(dev) -> None:
