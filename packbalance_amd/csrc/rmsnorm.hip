@@ -62,15 +62,30 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_reg(
   const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
   if (row >= rows) return;
   const TX *xr = x + row * xs;
+  // x is streamed (non-temporal: read once); w is re-read by every row and
+  // stays cached.  All loads are issued before the reduction.
+  u32x4 raw[NV];
+  float wv[NV][VEC];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = (i * 64 + lane) * VEC;
+    if (c < n) {
+      raw[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(xr + c));
+      load_vec<TW, VEC>(w + c, wv[i]);
+    }
+  }
   float v[NV][VEC];
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = (i * 64 + lane) * VEC;
     if (c < n) {
-      load_vec<TX, VEC>(xr + c, v[i]);
+      const TX *e = reinterpret_cast<const TX *>(&raw[i]);
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) ss += v[i][e] * v[i][e];
+      for (int k = 0; k < VEC; ++k) {
+        v[i][k] = to_f32(e[k]);
+        ss += v[i][k] * v[i][k];
+      }
     }
   }
   ss = wave_sum(ss);
@@ -81,12 +96,10 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_reg(
   for (int i = 0; i < NV; ++i) {
     const int c = (i * 64 + lane) * VEC;
     if (c < n) {
-      float wv[VEC];
-      load_vec<TW, VEC>(w + c, wv);
       float o[VEC];
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) o[e] = v[i][e] * r * wv[e];
-      store_vec<TX, VEC>(yr + c, o);
+      for (int e = 0; e < VEC; ++e) o[e] = v[i][e] * r * wv[i][e];
+      store16_nt<TX>(yr + c, o);
     }
   }
 }
@@ -114,8 +127,13 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_loop(
 
 // ---------------------------------------------------------------- backward
 // Each workgroup owns rows [blockIdx.x*rows_per_wg, ...), its waves take
-// every kWaves-th row; dw partials are reduced across the waves in LDS and
-// written as one fp32 row per workgroup.
+// every kWaves-th row.  Per row a wave streams x and dy once (non-temporal,
+// kept as raw 16-byte vectors), forms dot = sum(dy*w*x_hat) and the dw
+// partial in one pass over the registers, and dx = r*(dy*w - x_hat*dot) in a
+// second; w is loaded once per wave.  Without a register prefetch of the next
+// row the kernel needs ~170 registers, so more waves per CU keep the loads in
+// flight.  dw partials are reduced across the waves in LDS and written as one
+// fp32 row per workgroup.
 template <typename TX, typename TW, int NV>
 __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_reg(
     const TX *__restrict__ dy, int64_t dys, const TX *__restrict__ x, int64_t xs,
@@ -126,69 +144,69 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_reg(
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const float inv_n = 1.0f / (float)n;
+  // w stays packed in its own type (VEC elements per lane and vector) and is
+  // widened where it is used.
+  constexpr int WB = VEC * sizeof(TW);  // bytes of w per vector
+  typedef unsigned wraw_t __attribute__((ext_vector_type(WB / 4)));
   float acc[NV][VEC];
+  wraw_t wraw[NV];
 #pragma unroll
-  for (int i = 0; i < NV; ++i)
+  for (int i = 0; i < NV; ++i) {
+    const int c = (i * 64 + lane) * VEC;
+    if (c < n) wraw[i] = *reinterpret_cast<const wraw_t *>(w + c);
 #pragma unroll
     for (int e = 0; e < VEC; ++e) acc[i][e] = 0.f;
+  }
+  auto wv = [&](int i, int e) { return to_f32(reinterpret_cast<const TW *>(&wraw[i])[e]); };
 
   const int64_t r0 = (int64_t)blockIdx.x * rows_per_wg;
   const int64_t r1 = r0 + rows_per_wg < rows ? r0 + rows_per_wg : rows;
-  // Raw 16-byte vectors of the next row, loaded while this row is computed.
-  u32x4 nx[NV], nd[NV];
-  auto prefetch = [&](int64_t row) {
+#pragma unroll 1
+  for (int64_t row = r0 + wave; row < r1; row += kWaves) {
+    u32x4 cx[NV], cd[NV];
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int c = (i * 64 + lane) * VEC;
       if (c < n) {
-        nx[i] = *reinterpret_cast<const u32x4 *>(x + row * xs + c);
-        nd[i] = *reinterpret_cast<const u32x4 *>(dy + row * dys + c);
+        cx[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(x + row * xs + c));
+        cd[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(dy + row * dys + c));
       }
     }
-  };
-  if (r0 + wave < r1) prefetch(r0 + wave);
-  for (int64_t row = r0 + wave; row < r1; row += kWaves) {
     const float r = rstd[row];
-    u32x4 cx[NV], cd[NV];
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      cx[i] = nx[i];
-      cd[i] = nd[i];
-    }
-    if (row + kWaves < r1) prefetch(row + kWaves);
-    float xh[NV][VEC], g[NV][VEC];
     float dot = 0.f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int c = (i * 64 + lane) * VEC;
       if (c < n) {
-        float dv[VEC], wv[VEC];
         const TX *ex = reinterpret_cast<const TX *>(&cx[i]);
         const TX *ed = reinterpret_cast<const TX *>(&cd[i]);
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
-          xh[i][e] = to_f32(ex[e]);
-          dv[e] = to_f32(ed[e]);
-        }
-        load_vec<TW, VEC>(w + c, wv);
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          xh[i][e] *= r;
-          g[i][e] = dv[e] * wv[e];
-          dot += g[i][e] * xh[i][e];
-          acc[i][e] += dv[e] * xh[i][e];
+          const float xh = to_f32(ex[e]) * r, dv = to_f32(ed[e]);
+          dot += dv * wv(i, e) * xh;
+          acc[i][e] += dv * xh;
         }
       }
     }
     dot = wave_sum(dot) * inv_n;
+    // Re-widen from the raw vectors instead of keeping 2*NV*VEC floats live
+    // across the reduction (the empty asm stops the compiler from reusing the
+    // first pass's values).
+#pragma unroll
+    for (int i = 0; i < NV; ++i) asm volatile("" : "+v"(cx[i]), "+v"(cd[i]));
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int c = (i * 64 + lane) * VEC;
       if (c < n) {
+        const TX *ex = reinterpret_cast<const TX *>(&cx[i]);
+        const TX *ed = reinterpret_cast<const TX *>(&cd[i]);
         float o[VEC];
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) o[e] = r * (g[i][e] - xh[i][e] * dot);
-        store_vec<TX, VEC>(dx + row * dxs + c, o);
+        for (int e = 0; e < VEC; ++e) {
+          const float xh = to_f32(ex[e]) * r;
+          o[e] = r * (to_f32(ed[e]) * wv(i, e) - xh * dot);
+        }
+        store16_nt<TX>(dx + row * dxs + c, o);
       }
     }
   }
@@ -293,10 +311,11 @@ struct BwdPlan {
 };
 
 BwdPlan bwd_plan(int64_t rows) {
-  // Aim for ~1024 workgroups (4 per CU) so the partial rows stay a small
-  // fraction of the traffic; at least 2 rows per wave so the next-row
-  // prefetch has something to overlap.
-  int64_t rpw = (rows + 1023) / 1024;
+  // Aim for 512 workgroups: one resident round at two 4-wave workgroups per
+  // CU (the register-resident backward runs two waves per SIMD); measured
+  // at [32768, 4096] bf16: 512 -> 4.98 TB/s, 768 -> 4.21, 1024 -> 4.78,
+  // 2048 -> 4.62.  The fp32 partial rows stay ~4% of the traffic.
+  int64_t rpw = (rows + 511) / 512;
   if (rpw < 2 * kWaves) rpw = 2 * kWaves;
   BwdPlan p;
   p.rows_per_wg = (int)rpw;

@@ -4,9 +4,9 @@
 //   fwd  y  = g*s*u                       s = sigmoid(g)
 //   bwd  dg = dy*u*s*(1 + g*(1-s)),  du = dy*g*s
 // Pure streaming: every lane moves 16-byte vectors (8 bf16 or 4 fp32) with
-// non-temporal hints (each byte is touched once), a grid-stride loop keeps a
-// fixed number of waves resident, and the sigmoid runs on the hardware
-// exp2/rcp units so the kernel stays bound by HBM, not by the VALU.
+// non-temporal hints (each byte is touched once), several vectors per lane in
+// flight, and the sigmoid runs on the hardware exp2/rcp units so the kernel
+// stays bound by HBM, not by the VALU.
 #include "common.hpp"
 
 namespace pb {
@@ -14,45 +14,85 @@ namespace {
 
 constexpr int kThreads = 256;
 
-template <typename T>
+// U 16-byte vectors per thread, all loads issued before any math, one pass
+// over the data (no grid-stride loop): measured on MI355X, streaming with
+// non-temporal loads and stores at 4-8 vectors per thread reaches ~6 TB/s
+// for a copy, against ~5 TB/s with one vector per thread in a grid-stride
+// loop or with plain (cached) loads.
+template <typename T, int U>
 __global__ __launch_bounds__(kThreads) void swiglu_fwd_vec(const T *__restrict__ gate,
                                                            const T *__restrict__ up,
                                                            T *__restrict__ out, int64_t nvec) {
   constexpr int VEC = 16 / sizeof(T);
-  const int64_t stride = (int64_t)gridDim.x * kThreads;
-  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < nvec; i += stride) {
-    float g[VEC], u[VEC], y[VEC];
-    load16_nt<T>(gate + i * VEC, g);
-    load16_nt<T>(up + i * VEC, u);
+  const int64_t base = (int64_t)blockIdx.x * kThreads * U + threadIdx.x;
+  u32x4 g[U], u[U];
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) y[e] = g[e] * sigmoid(g[e]) * u[e];
-    store16_nt<T>(out + i * VEC, y);
+  for (int k = 0; k < U; ++k) {
+    const int64_t i = base + (int64_t)k * kThreads;
+    if (i < nvec) {
+      g[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(gate) + i);
+      u[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(up) + i);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < U; ++k) {
+    const int64_t i = base + (int64_t)k * kThreads;
+    if (i < nvec) {
+      const T *ge = reinterpret_cast<const T *>(&g[k]);
+      const T *ue = reinterpret_cast<const T *>(&u[k]);
+      float y[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float gv = to_f32(ge[e]);
+        y[e] = gv * sigmoid(gv) * to_f32(ue[e]);
+      }
+      store16_nt<T>(out + i * VEC, y);
+    }
   }
 }
 
-template <typename T>
+template <typename T, int U>
 __global__ __launch_bounds__(kThreads) void swiglu_bwd_vec(const T *__restrict__ gate,
                                                            const T *__restrict__ up,
                                                            const T *__restrict__ dy,
                                                            T *__restrict__ dgate,
                                                            T *__restrict__ dup, int64_t nvec) {
   constexpr int VEC = 16 / sizeof(T);
-  const int64_t stride = (int64_t)gridDim.x * kThreads;
-  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < nvec; i += stride) {
-    float g[VEC], u[VEC], d[VEC], dg[VEC], du[VEC];
-    load16_nt<T>(gate + i * VEC, g);
-    load16_nt<T>(up + i * VEC, u);
-    load16_nt<T>(dy + i * VEC, d);
+  const int64_t base = (int64_t)blockIdx.x * kThreads * U + threadIdx.x;
+  u32x4 g[U], u[U], d[U];
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      const float s = sigmoid(g[e]);
-      dg[e] = d[e] * u[e] * (s * (1.0f + g[e] * (1.0f - s)));
-      du[e] = d[e] * (g[e] * s);
+  for (int k = 0; k < U; ++k) {
+    const int64_t i = base + (int64_t)k * kThreads;
+    if (i < nvec) {
+      g[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(gate) + i);
+      u[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(up) + i);
+      d[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(dy) + i);
     }
-    store16_nt<T>(dgate + i * VEC, dg);
-    store16_nt<T>(dup + i * VEC, du);
+  }
+#pragma unroll
+  for (int k = 0; k < U; ++k) {
+    const int64_t i = base + (int64_t)k * kThreads;
+    if (i < nvec) {
+      const T *ge = reinterpret_cast<const T *>(&g[k]);
+      const T *ue = reinterpret_cast<const T *>(&u[k]);
+      const T *de = reinterpret_cast<const T *>(&d[k]);
+      float dg[VEC], du[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float gv = to_f32(ge[e]), uv = to_f32(ue[e]), dv = to_f32(de[e]);
+        const float sg = sigmoid(gv);
+        dg[e] = dv * uv * (sg * (1.0f + gv * (1.0f - sg)));
+        du[e] = dv * (gv * sg);
+      }
+      store16_nt<T>(dgate + i * VEC, dg);
+      store16_nt<T>(dup + i * VEC, du);
+    }
   }
 }
+
+constexpr int kFwdU = 8;
+constexpr int kBwdU = 4;
+constexpr int64_t kMaxVecPerLaunch = 1LL << 30;
 
 // Scalar tail / unaligned path.
 template <typename T>
@@ -90,6 +130,10 @@ unsigned grid_for(int64_t items) {
   return (unsigned)(g < cap ? (g > 0 ? g : 1) : cap);
 }
 
+unsigned one_pass_grid(int64_t nvec, int u) {
+  return (unsigned)((nvec + (int64_t)kThreads * u - 1) / ((int64_t)kThreads * u));
+}
+
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 template <typename T>
@@ -101,7 +145,12 @@ int fwd_typed(const void *g, const void *u, void *o, int64_t n, hipStream_t st) 
   int64_t nvec = 0;
   if (aligned16(g) && aligned16(u) && aligned16(o)) {
     nvec = n / VEC;
-    if (nvec) hipLaunchKernelGGL((swiglu_fwd_vec<T>), dim3(grid_for(nvec)), dim3(kThreads), 0, st, G, U, O, nvec);
+    // Launches of at most 2^30 vectors (grid.x stays far below 2^31).
+    for (int64_t v0 = 0; v0 < nvec; v0 += kMaxVecPerLaunch) {
+      const int64_t nv = nvec - v0 < kMaxVecPerLaunch ? nvec - v0 : kMaxVecPerLaunch;
+      hipLaunchKernelGGL((swiglu_fwd_vec<T, kFwdU>), dim3(one_pass_grid(nv, kFwdU)), dim3(kThreads),
+                         0, st, G + v0 * VEC, U + v0 * VEC, O + v0 * VEC, nv);
+    }
   }
   if (nvec * VEC < n)
     hipLaunchKernelGGL((swiglu_fwd_scalar<T>), dim3(grid_for(n - nvec * VEC)), dim3(kThreads), 0, st,
@@ -121,8 +170,12 @@ int bwd_typed(const void *g, const void *u, const void *d, void *dg, void *du, i
   int64_t nvec = 0;
   if (aligned16(g) && aligned16(u) && aligned16(d) && aligned16(dg) && aligned16(du)) {
     nvec = n / VEC;
-    if (nvec)
-      hipLaunchKernelGGL((swiglu_bwd_vec<T>), dim3(grid_for(nvec)), dim3(kThreads), 0, st, G, U, D, DG, DU, nvec);
+    for (int64_t v0 = 0; v0 < nvec; v0 += kMaxVecPerLaunch) {
+      const int64_t nv = nvec - v0 < kMaxVecPerLaunch ? nvec - v0 : kMaxVecPerLaunch;
+      const int64_t o = v0 * VEC;
+      hipLaunchKernelGGL((swiglu_bwd_vec<T, kBwdU>), dim3(one_pass_grid(nv, kBwdU)),
+                         dim3(kThreads), 0, st, G + o, U + o, D + o, DG + o, DU + o, nv);
+    }
   }
   if (nvec * VEC < n)
     hipLaunchKernelGGL((swiglu_bwd_scalar<T>), dim3(grid_for(n - nvec * VEC)), dim3(kThreads), 0, st,
