@@ -26,6 +26,9 @@
 //                   operands are read from the row-major LDS tiles with
 //                   ds_read_b64_tr_b16, and the next tile is prefetched into
 //                   registers while the current one is computed.
+#include <algorithm>
+#include <type_traits>
+
 #include "attn_common.hpp"
 
 namespace pb {
@@ -208,6 +211,339 @@ __global__ __launch_bounds__(64 * WAVES) void attn_bwd_dkdv(BwdArgs a) {
         } else {
           a.dk.row(b, hk, kvr)[d] = (bf16_t)(dk_acc[db][j] * a.scale);
           a.dv.row(b, hk, kvr)[d] = (bf16_t)dv_acc[db][j];
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- dK, dV (pipelined)
+// Grid decode of the KV-major kernel for L2 reuse: workgroup i runs on XCD
+// i % 8; each XCD takes whole (pack, KV head[, member]) pairs and walks their
+// KV tiles in order, so the workgroups resident on one XCD stream the same
+// Q / dO rows through its L2 (each KV tile reads every query tile at or after
+// it).  Identity map when the pair count is not a multiple of 8.
+__device__ __forceinline__ void decode_kv_major(int bid, int nkt, int npairs, int &kt, int &pair) {
+  if (npairs % 8 == 0) {
+    const int x = bid & 7, j = bid >> 3;
+    pair = (j / nkt) * 8 + x;
+    kt = j - (j / nkt) * nkt;
+  } else {
+    pair = bid / nkt;
+    kt = bid - pair * nkt;
+  }
+}
+
+// One step of the pipelined dK/dV walk: query head, first query row, plan
+// entry.  (Declared at namespace scope: a struct local to the kernel template
+// keeps clang from emitting the kernel's host stub.)
+struct DkdvStep {
+  int h, q0, e;
+};
+
+// Pipelined dK/dV (16-byte aligned views and documents, D == DP in {64, 128},
+// sequence a multiple of 64).  Wave w owns 32 KV rows with K and V fragments
+// in registers and dK/dV accumulators.  The workgroup walks steps t = (query
+// sub-tile of 32 rows, query head of the group), sub-tile outer: per step
+// S = Q K^T and dP = dO V^T (lane <-> KV row), P = exp2(S*scale*log2e -
+// lse), dS = P*(dP - delta), then dV += P^T dO and dK += dS^T Q with the Q /
+// dO column fragments read by ds_read_b64_tr_b16 from the same swizzled LDS
+// tiles the row fragments come from.  Q, dO, lse/delta and the query
+// documents arrive by DMA through a 4-slot ring (steps t+1 .. t+3 in flight
+// while t is computed, one barrier per step); the MFMAs of S(t+1) and
+// dP(t+1) are interleaved with the P/dS math of step t.
+template <int DP, int WAVES, bool SPLIT>
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void attn_bwd_dkdv_pipe(BwdArgs a) {
+  constexpr int NT = 64 * WAVES, BN = 32 * WAVES;
+  constexpr int NDK = DP / 16, NDB = DP / 32;
+  constexpr int HB = 32 * DP * 2;  // bytes of one 32-row sub-tile
+  using Dma = TileDma<DP, 32, NT>;
+  constexpr int NDMA = Dma::NDMA;
+  constexpr int NVF = 2 * NDB;  // column fragments of one operand per step
+  // Ring slots are separate LDS objects (see attn_fwd_pipe).
+  __shared__ __align__(16) char qs0[HB], qs1[HB], qs2[HB], qs3[HB];
+  __shared__ __align__(16) char gs0[HB], gs1[HB], gs2[HB], gs3[HB];
+  __shared__ __align__(16) float ld0[64], ld1[64], ld2[64], ld3[64];  // lse[32], delta[32]
+  __shared__ __align__(16) int64_t qd0[32], qd1[32], qd2[32], qd3[32];
+  auto qslot = [&](auto Rc) -> char * {
+    constexpr int R = decltype(Rc)::value;
+    if constexpr (R == 0) return qs0; else if constexpr (R == 1) return qs1;
+    else if constexpr (R == 2) return qs2; else return qs3;
+  };
+  auto gslot = [&](auto Rc) -> char * {
+    constexpr int R = decltype(Rc)::value;
+    if constexpr (R == 0) return gs0; else if constexpr (R == 1) return gs1;
+    else if constexpr (R == 2) return gs2; else return gs3;
+  };
+  auto lslot = [&](auto Rc) -> float * {
+    constexpr int R = decltype(Rc)::value;
+    if constexpr (R == 0) return ld0; else if constexpr (R == 1) return ld1;
+    else if constexpr (R == 2) return ld2; else return ld3;
+  };
+  auto dslot = [&](auto Rc) -> int64_t * {
+    constexpr int R = decltype(Rc)::value;
+    if constexpr (R == 0) return qd0; else if constexpr (R == 1) return qd1;
+    else if constexpr (R == 2) return qd2; else return qd3;
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hh = lane >> 5, l32 = lane & 31;
+  const int Gfull = a.Hq / a.Hkv;
+  const int G = SPLIT ? 1 : Gfull;
+  int kt, pair;
+  decode_kv_major((int)blockIdx.x, a.nkt_kv, a.B * a.Hkv * (SPLIT ? Gfull : 1), kt, pair);
+  const int g0 = SPLIT ? pair % Gfull : 0;
+  const int bh = SPLIT ? pair / Gfull : pair;
+  const int b = bh / a.Hkv, hk = bh - (bh / a.Hkv) * a.Hkv;
+  const int S = a.S;
+  const int64_t *docb = a.doc + b * a.doc_sb;
+  const float sl2 = a.sl2;
+
+  const int kv = kt * BN + wave * 32 + l32;
+  const bool kvvalid = kv < S;
+  const int kvr = kvvalid ? kv : S - 1;
+  const int64_t kvdoc = docb[kvr];
+  bf16x8_t kf[NDK], vf[NDK];
+  {
+    const bf16_t *krow = a.k.row(b, hk, kvr), *vrow = a.v.row(b, hk, kvr);
+#pragma unroll
+    for (int dk = 0; dk < NDK; ++dk) {
+      kf[dk] = *reinterpret_cast<const bf16x8_t *>(krow + 16 * dk + 8 * hh);
+      vf[dk] = *reinterpret_cast<const bf16x8_t *>(vrow + 16 * dk + 8 * hh);
+    }
+  }
+  f32x16_t dk_acc[NDB], dv_acc[NDB];
+#pragma unroll
+  for (int i = 0; i < NDB; ++i) {
+    dk_acc[i] = zero16();
+    dv_acc[i] = zero16();
+  }
+
+  uint32_t qoff[NDMA], goff[NDMA];
+  Dma::offsets(a.q.ss, wave, lane, qoff);
+  Dma::offsets(a.dout.ss, wave, lane, goff);
+  // Per-lane fragment offsets within a sub-tile (see attn_fwd_pipe).
+  int roffs[NDK], coffs[NDB][2];
+  {
+    const int j = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int dk = 0; dk < NDK; ++dk) {
+      roffs[dk] = SwzTile<DP>::off(l32, 16 * dk + 8 * hh);
+      asm volatile("" : "+v"(roffs[dk]));
+    }
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const int col = 32 * db + 16 * (g & 1) + 4 * (j & 3);
+      const int row = 4 * hh + (j >> 2);
+      coffs[db][0] = SwzTile<DP>::off(row, col);
+      coffs[db][1] = SwzTile<DP>::off(row + 8, col);
+      asm volatile("" : "+v"(coffs[db][0]), "+v"(coffs[db][1]));
+    }
+  }
+  auto rfrag = [&](const char *t, int dk) {
+    return *reinterpret_cast<const bf16x8_t *>(t + roffs[dk]);
+  };
+  auto cfrag = [&](const char *t, int f) {  // f = qk * NDB + db
+    const char *base = t + (f / NDB) * 16 * DP * 2;
+    const int db = f % NDB;
+    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(base + coffs[db][0]));
+    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(base + coffs[db][1]));
+    typedef short i16x8_t __attribute__((ext_vector_type(8)));
+    i16x8_t r = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return *reinterpret_cast<bf16x8_t *>(&r);
+  };
+
+  const int cnt = a.kcnt[b * a.nkt_kv + kt];
+  const int U = 2 * cnt;  // 32-row query sub-tiles
+  const int T = G * U;    // steps: sub-tile outer, head of the group inner
+  const int32_t *lst = a.klist + ((int64_t)b * a.nkt_kv + kt) * a.nqt_kv;
+  // Step t -> (query head, first query row, plan entry); steps past the last
+  // repeat it (their DMA lands in slots nobody reads any more).
+  auto step_of = [&](int t, int e) {
+    const int tc = t < T ? t : T - 1;
+    const int u = tc / G, g = tc - (tc / G) * G;
+    DkdvStep s;
+    s.h = hk * Gfull + g0 + g;
+    s.e = e;
+    s.q0 = plan_tile(e) * kQStep + 32 * (u & 1);
+    return s;
+  };
+  auto entry = [&](int t) {
+    const int tc = t < T ? t : T - 1;
+    return lst[(tc / G) >> 1];
+  };
+
+  // DMA of one step: lse/delta (wave 0) and query documents (wave 1 % W)
+  // first, then the Q and dO sub-tiles.
+  auto dma_step = [&](const DkdvStep &s, auto Rc) {
+    const int64_t ro = ((int64_t)b * a.Hq + s.h) * S + s.q0;
+    if (wave == 0 && lane < 16) {
+      const float *src = lane < 8 ? a.lse + ro + 4 * lane : a.delta + ro + 4 * (lane - 8);
+      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lslot(Rc), 16, 0, 0);
+    }
+    if (wave == (WAVES > 1 ? 1 : 0) && lane < 16)
+      __builtin_amdgcn_global_load_lds(docb + s.q0 + 2 * lane,
+                                       (__attribute__((address_space(3))) void *)dslot(Rc), 16, 0, 0);
+    Dma::copy(reinterpret_cast<const char *>(a.q.row(b, s.h, 0)), a.q.ss, qoff, s.q0, qslot(Rc), wave);
+    Dma::copy(reinterpret_cast<const char *>(a.dout.row(b, s.h, 0)), a.dout.ss, goff, s.q0,
+              gslot(Rc), wave);
+  };
+
+  // Element mask of a PARTIAL step: same document, kv <= q (q < S always).
+  auto mask = [&](f32x16_t &sv, int q0, const int64_t *qd) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int qr = 8 * (j >> 2) + 4 * hh + (j & 3);
+      const bool ok = kvvalid && kv <= q0 + qr && qd[qr] == kvdoc;
+      sv[j] = ok ? sv[j] : -INFINITY;
+    }
+  };
+
+  // P and dS of one step for elements j, j+1 (query rows 8(j/4) + 4hh + j%4).
+  // The packed results pass through an empty volatile asm so they are formed
+  // where this call sits in the MFMA schedule, not sunk towards their use.
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  auto pds2 = [&](int j, const f32x16_t &sc, const f32x16_t &pc, const float (&lse)[16],
+                  const float (&dlt)[16], bf16x8_t (&pf)[2], bf16x8_t (&dsf)[2]) {
+    bf16x2_t pp, dd;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const float p = fast_exp2(fmaf(sc[j + i], sl2, -lse[j + i]));
+      pp[i] = (bf16_t)p;
+      dd[i] = (bf16_t)(p * (pc[j + i] - dlt[j + i]));
+    }
+    asm volatile("" ::"v"(*reinterpret_cast<uint32_t *>(&pp)), "v"(*reinterpret_cast<uint32_t *>(&dd)));
+    pf[j >> 3][j & 7] = pp[0];
+    pf[j >> 3][(j & 7) + 1] = pp[1];
+    dsf[j >> 3][j & 7] = dd[0];
+    dsf[j >> 3][(j & 7) + 1] = dd[1];
+  };
+  auto load_ld = [&](const float *ld, float (&lse)[16], float (&dlt)[16]) {
+#pragma unroll
+    for (int jg = 0; jg < 4; ++jg) {
+      const float4 l4 = *reinterpret_cast<const float4 *>(ld + 8 * jg + 4 * hh);
+      const float4 d4 = *reinterpret_cast<const float4 *>(ld + 32 + 8 * jg + 4 * hh);
+      lse[4 * jg] = l4.x; lse[4 * jg + 1] = l4.y; lse[4 * jg + 2] = l4.z; lse[4 * jg + 3] = l4.w;
+      dlt[4 * jg] = d4.x; dlt[4 * jg + 1] = d4.y; dlt[4 * jg + 2] = d4.z; dlt[4 * jg + 3] = d4.w;
+    }
+  };
+  auto dvdk = [&](int f, const bf16x8_t &gcol, const bf16x8_t &qcol, const bf16x8_t (&pf)[2],
+                  const bf16x8_t (&dsf)[2]) {
+    dv_acc[f % NDB] = mfma32(pf[f / NDB], gcol, dv_acc[f % NDB]);
+    dk_acc[f % NDB] = mfma32(dsf[f / NDB], qcol, dk_acc[f % NDB]);
+  };
+
+  if (T > 0) {
+    // Plan entries of steps t+1 .. t+4 for body t (loaded one body ahead).
+    int ew[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ew[i] = entry(i + 1);
+    const int e0 = entry(0);
+    dma_step(step_of(0, e0), I0());
+    dma_step(step_of(1, ew[0]), I1());
+    dma_step(step_of(2, ew[1]), I2());
+    wait_vmcnt<0>();
+    __syncthreads();
+    f32x16_t sc = zero16(), pc = zero16();
+#pragma unroll
+    for (int dk = 0; dk < NDK; ++dk) {
+      sc = mfma32(rfrag(qs0, dk), kf[dk], sc);
+      pc = mfma32(rfrag(gs0, dk), vf[dk], pc);
+    }
+    if (!plan_full(e0)) mask(sc, step_of(0, e0).q0, qd0);
+
+    auto body = [&](auto Rc, int t) {
+      constexpr int R = decltype(Rc)::value;
+      using IR = std::integral_constant<int, R>;
+      using IR1 = std::integral_constant<int, (R + 1) % 4>;
+      using IR3 = std::integral_constant<int, (R + 3) % 4>;
+      const int e1 = __builtin_amdgcn_readfirstlane(ew[0]);
+      const int e3 = __builtin_amdgcn_readfirstlane(ew[2]);
+      const int e4 = entry(t + 5);  // for body t + 1, issued before this body's DMA
+      __builtin_amdgcn_sched_barrier(0);
+      dma_step(step_of(t + 3, e3), IR3());
+      // Step t's lse/delta, step t+1's Q / dO row fragments.
+      float lse[16], dlt[16];
+      load_ld(lslot(IR()), lse, dlt);
+      bf16x8_t qa[NDK], ga[NDK];
+#pragma unroll
+      for (int dk = 0; dk < NDK; ++dk) {
+        qa[dk] = rfrag(qslot(IR1()), dk);
+        ga[dk] = rfrag(gslot(IR1()), dk);
+      }
+      f32x16_t sn = zero16(), pn = zero16();
+      bf16x8_t pf[2], dsf[2];
+      __builtin_amdgcn_sched_barrier(0);
+      // S(t+1), dP(t+1) MFMAs with the P/dS math of step t between them.
+      constexpr int JPS = 16 / NDK;  // elements per head-dim step (2 or 4)
+#pragma unroll
+      for (int dk = 0; dk < NDK; ++dk) {
+        sn = mfma32(qa[dk], kf[dk], sn);
+        pn = mfma32(ga[dk], vf[dk], pn);
+#pragma unroll
+        for (int j = dk * JPS; j < (dk + 1) * JPS; j += 2) pds2(j, sc, pc, lse, dlt, pf, dsf);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // dV(t) += P^T dO(t), dK(t) += dS^T Q(t); S(t+1) moves into sc alongside.
+#pragma unroll
+      for (int f = 0; f < NVF; ++f)
+        dvdk(f, cfrag(gslot(IR()), f), cfrag(qslot(IR()), f), pf, dsf);
+      sc = sn;
+      pc = pn;
+      if (!plan_full(e1)) mask(sc, step_of(t + 1, e1).q0, dslot(IR1()));
+      wait_vmcnt<2 * NDMA>();
+      block_sync_nofence();
+      ew[0] = ew[1];
+      ew[1] = ew[2];
+      ew[2] = ew[3];
+      ew[3] = e4;
+    };
+    int t = 0;
+    for (; t + 4 < T; t += 4) {
+      body(I0(), t);
+      body(I1(), t + 1);
+      body(I2(), t + 2);
+      body(I3(), t + 3);
+    }
+    if (t + 1 < T) { body(I0(), t); ++t; }
+    if (t + 1 < T) { body(I1(), t); ++t; }
+    if (t + 1 < T) { body(I2(), t); ++t; }
+    wait_vmcnt<0>();
+    // Last step: no S(t+1).
+    const int rl = t & 3;
+    const char *qt = rl == 0 ? qs0 : rl == 1 ? qs1 : rl == 2 ? qs2 : qs3;
+    const char *gt = rl == 0 ? gs0 : rl == 1 ? gs1 : rl == 2 ? gs2 : gs3;
+    const float *lt = rl == 0 ? ld0 : rl == 1 ? ld1 : rl == 2 ? ld2 : ld3;
+    float lse[16], dlt[16];
+    load_ld(lt, lse, dlt);
+    bf16x8_t pf[2], dsf[2];
+#pragma unroll
+    for (int j = 0; j < 16; j += 2) pds2(j, sc, pc, lse, dlt, pf, dsf);
+#pragma unroll
+    for (int f = 0; f < NVF; ++f) dvdk(f, cfrag(gt, f), cfrag(qt, f), pf, dsf);
+  }
+
+  // Accumulators: lane <-> head-dim column, register j <-> KV row of the wave.
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+    const int d = 32 * db + l32;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int kvw = kt * BN + wave * 32 + 8 * (j >> 2) + 4 * hh + (j & 3);
+      if (kvw < S) {
+        if constexpr (SPLIT) {
+          const int64_t o = (((int64_t)b * a.Hq + hk * Gfull + g0) * S + kvw) * a.D + d;
+          a.dk_part[o] = dk_acc[db][j];
+          a.dv_part[o] = dv_acc[db][j];
+        } else {
+          a.dk.row(b, hk, kvw)[d] = (bf16_t)(dk_acc[db][j] * a.scale);
+          a.dv.row(b, hk, kvw)[d] = (bf16_t)dv_acc[db][j];
         }
       }
     }
@@ -456,7 +792,20 @@ extern "C" int pb_attn_bwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v,
   if (cfg.dq_waves == 4) PB_BY_D(PB_DQ, 4); else PB_BY_D(PB_DQ, 2);
   rc = launch_status("pb_attn_bwd(dq)");
   if (rc) return rc;
-  if (cfg.kv_waves == 4) PB_BY_D(PB_KV, 4, false);
+  // DMA-pipelined dK/dV where views, documents and the sequence length allow.
+  const bool pipe = a.vec && (d == 64 || d == 128) && s % 64 == 0 &&
+                    (reinterpret_cast<uintptr_t>(doc_ids) & 15) == 0 && doc_stride % 2 == 0 &&
+                    (reinterpret_cast<uintptr_t>(lse) & 15) == 0 &&
+                    (reinterpret_cast<uintptr_t>(workspace) & 15) == 0 &&
+                    32 * std::max(q->stride_s, dout->stride_s) < (1LL << 30);
+  if (pipe) {
+#define PB_KVP(DP, W, SP) \
+  hipLaunchKernelGGL((attn_bwd_dkdv_pipe<DP, W, SP>), g_kv, dim3(64 * W), 0, st, a)
+    if (cfg.kv_waves == 4) { if (d == 128) PB_KVP(128, 4, false); else PB_KVP(64, 4, false); }
+    else if (cfg.split) { if (d == 128) PB_KVP(128, 2, true); else PB_KVP(64, 2, true); }
+    else { if (d == 128) PB_KVP(128, 2, false); else PB_KVP(64, 2, false); }
+#undef PB_KVP
+  } else if (cfg.kv_waves == 4) PB_BY_D(PB_KV, 4, false);
   else if (cfg.split) PB_BY_D(PB_KV, 2, true);
   else PB_BY_D(PB_KV, 2, false);
 #undef PB_BY_D
