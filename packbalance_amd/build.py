@@ -73,6 +73,21 @@ def is_stale() -> bool:
     return any(p.stat().st_mtime > t for p in sources() + _headers())
 
 
+def _check_kernel_stubs(lib: Path) -> None:
+    """Fail the build when a kernel's host stub is referenced but missing.
+
+    clang's HIP host pass can silently omit the stub of a __global__ template
+    (seen with a struct declared inside the kernel, or a lambda call inside a
+    generic lambda's builtin argument); the library then links but fails to
+    load with an undefined __device_stub__ symbol.
+    """
+    nm = shutil.which("nm") or "/opt/rocm/llvm/bin/llvm-nm"
+    res = subprocess.run([nm, "-D", "--undefined-only", str(lib)], capture_output=True, text=True)
+    missing = [ln.split()[-1] for ln in res.stdout.splitlines() if "__device_stub__" in ln]
+    if missing:
+        raise RuntimeError("kernel host stubs missing from the library: " + ", ".join(missing))
+
+
 def build(jobs: int | None = None, verbose: bool = False) -> Path:
     BUILD.mkdir(exist_ok=True)
     srcs = sources()
@@ -84,6 +99,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
+    _check_kernel_stubs(tmp)
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB} from {len(srcs)} sources", flush=True)

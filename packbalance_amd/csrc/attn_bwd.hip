@@ -691,6 +691,250 @@ __device__ __forceinline__ void dq_body(const BwdArgs &a) {
     }
 }
 
+// ---------------------------------------------------------------- dQ (pipelined)
+// Pipelined dQ (same eligibility as attn_bwd_dkdv_pipe).  Lane <-> query row
+// as in the forward: Q and dO fragments in registers, D = rowsum(dO * O) from
+// them (written for the dK/dV kernel).  The plan's KV tiles are walked as
+// 32-row sub-tiles u; K, V and the KV documents arrive by DMA through a
+// 4-slot ring of swizzled tiles (three sub-tiles in flight).  Body u issues
+// the MFMAs of S(u+1)^T = K Q^T and dP(u+1)^T = V dO^T between the P/dS math
+// of sub-tile u, then dQ^T += K^T dS^T with K^T as column fragments of the
+// same K tile.  Head dim 64 fits two waves per SIMD (~214 registers); head
+// dim 128 needs ~320 and runs one.
+template <int DP, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(DP == 64 ? 2 : 1, DP == 64 ? 2 : 1)))
+void attn_bwd_dq_pipe(BwdArgs a) {
+  constexpr int NT = 64 * WAVES, BM = 32 * WAVES;
+  constexpr int NDK = DP / 16, NDB = DP / 32;
+  constexpr int HB = 32 * DP * 2;
+  using Dma = TileDma<DP, 32, NT>;
+  constexpr int NDMA = Dma::NDMA;
+  constexpr int NVF = 2 * NDB;
+  __shared__ __align__(16) char ks0[HB], ks1[HB], ks2[HB], ks3[HB];
+  __shared__ __align__(16) char vs0[HB], vs1[HB], vs2[HB], vs3[HB];
+  __shared__ __align__(16) int64_t kd0[32], kd1[32], kd2[32], kd3[32];
+  auto kslot = [&](auto Rc) -> char * {
+    constexpr int R = decltype(Rc)::value;
+    if constexpr (R == 0) return ks0; else if constexpr (R == 1) return ks1;
+    else if constexpr (R == 2) return ks2; else return ks3;
+  };
+  auto vslot = [&](auto Rc) -> char * {
+    constexpr int R = decltype(Rc)::value;
+    if constexpr (R == 0) return vs0; else if constexpr (R == 1) return vs1;
+    else if constexpr (R == 2) return vs2; else return vs3;
+  };
+  auto dslot = [&](auto Rc) -> int64_t * {
+    constexpr int R = decltype(Rc)::value;
+    if constexpr (R == 0) return kd0; else if constexpr (R == 1) return kd1;
+    else if constexpr (R == 2) return kd2; else return kd3;
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hh = lane >> 5, l32 = lane & 31;
+  int qt, b, h;
+  decode_q_major((int)blockIdx.x, a.nqt_dq, a.B, a.Hq, a.Hkv, qt, b, h);
+  const int hk = h / (a.Hq / a.Hkv);
+  const int S = a.S;
+  const int64_t *docb = a.doc + b * a.doc_sb;
+  const float sl2 = a.sl2;
+  const char *Kb = reinterpret_cast<const char *>(a.k.row(b, hk, 0));
+  const char *Vb = reinterpret_cast<const char *>(a.v.row(b, hk, 0));
+
+  const int qi = qt * BM + wave * 32 + l32;
+  const bool qvalid = qi < S;
+  const int qr = qvalid ? qi : S - 1;
+  const int64_t qdoc = docb[qr];
+  const int64_t row_o = ((int64_t)b * a.Hq + h) * S + qr;
+  const float lse2 = a.lse[row_o];
+  bf16x8_t qf[NDK], gf[NDK];
+  float dlt = 0.f;
+  {
+    const bf16_t *qrow = a.q.row(b, h, qr), *grow = a.dout.row(b, h, qr);
+    const bf16_t *orow = a.o.row(b, h, qr);
+#pragma unroll
+    for (int dk = 0; dk < NDK; ++dk) {
+      qf[dk] = *reinterpret_cast<const bf16x8_t *>(qrow + 16 * dk + 8 * hh);
+      gf[dk] = *reinterpret_cast<const bf16x8_t *>(grow + 16 * dk + 8 * hh);
+      const bf16x8_t of = *reinterpret_cast<const bf16x8_t *>(orow + 16 * dk + 8 * hh);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) dlt += (float)gf[dk][i] * (float)of[i];
+    }
+    dlt = xor32_sum(dlt);  // the lane halves hold complementary slices of the row
+    if (qvalid && hh == 0) a.delta[row_o] = dlt;
+  }
+  f32x16_t dq_acc[NDB];
+#pragma unroll
+  for (int i = 0; i < NDB; ++i) dq_acc[i] = zero16();
+
+  uint32_t koff[NDMA], voff[NDMA];
+  Dma::offsets(a.k.ss, wave, lane, koff);
+  Dma::offsets(a.v.ss, wave, lane, voff);
+  int roffs[NDK], coffs[NDB][2];
+  {
+    const int j = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int dk = 0; dk < NDK; ++dk) {
+      roffs[dk] = SwzTile<DP>::off(l32, 16 * dk + 8 * hh);
+      asm volatile("" : "+v"(roffs[dk]));
+    }
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const int col = 32 * db + 16 * (g & 1) + 4 * (j & 3);
+      const int row = 4 * hh + (j >> 2);
+      coffs[db][0] = SwzTile<DP>::off(row, col);
+      coffs[db][1] = SwzTile<DP>::off(row + 8, col);
+      asm volatile("" : "+v"(coffs[db][0]), "+v"(coffs[db][1]));
+    }
+  }
+  auto rfrag = [&](const char *t, int dk) {
+    return *reinterpret_cast<const bf16x8_t *>(t + roffs[dk]);
+  };
+  auto cfrag = [&](const char *t, int f) {  // f = kk * NDB + db
+    const char *base = t + (f / NDB) * 16 * DP * 2;
+    const int db = f % NDB;
+    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(base + coffs[db][0]));
+    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(base + coffs[db][1]));
+    typedef short i16x8_t __attribute__((ext_vector_type(8)));
+    i16x8_t r = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return *reinterpret_cast<bf16x8_t *>(&r);
+  };
+
+  const int cnt = a.qcnt[b * a.nqt_dq + qt];
+  const int U = 2 * cnt;
+  const int32_t *lst = a.qlist + ((int64_t)b * a.nqt_dq + qt) * a.nkt_dq;
+  auto entry = [&](int u) { return lst[(u < U ? u : U - 1) >> 1]; };
+  auto row0 = [&](int e, int u) { return plan_tile(e) * kKvStep + 32 * (u & 1); };
+  // (The row is passed in, not computed here: calling another lambda inside
+  // this generic lambda's DMA address makes clang drop the kernel's stub.)
+  auto dma_sub = [&](int kv0, auto Rc) {
+    if (wave == 0 && lane < 16)
+      __builtin_amdgcn_global_load_lds(docb + kv0 + 2 * lane,
+                                       (__attribute__((address_space(3))) void *)dslot(Rc), 16, 0, 0);
+    Dma::copy(Kb, a.k.ss, koff, kv0, kslot(Rc), wave);
+    Dma::copy(Vb, a.v.ss, voff, kv0, vslot(Rc), wave);
+  };
+  // Element mask of a PARTIAL sub-tile: same document and kv <= q.
+  auto mask = [&](f32x16_t &sv, int kv0, const int64_t *kd) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int kr = 8 * (j >> 2) + 4 * hh + (j & 3);
+      const bool ok = qvalid && kv0 + kr <= qi && kd[kr] == qdoc;
+      sv[j] = ok ? sv[j] : -INFINITY;
+    }
+  };
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  auto ds2 = [&](int j, const f32x16_t &sc, const f32x16_t &pc, bf16x8_t (&dsf)[2]) {
+    bf16x2_t dd;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const float p = fast_exp2(fmaf(sc[j + i], sl2, -lse2));
+      dd[i] = (bf16_t)(p * (pc[j + i] - dlt));
+    }
+    asm volatile("" ::"v"(*reinterpret_cast<uint32_t *>(&dd)));
+    dsf[j >> 3][j & 7] = dd[0];
+    dsf[j >> 3][(j & 7) + 1] = dd[1];
+  };
+
+  if (U > 0) {
+    int ew[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ew[i] = entry(i + 1);
+    const int e0 = entry(0);
+    dma_sub(row0(e0, 0), I0());
+    dma_sub(row0(ew[0], 1), I1());
+    dma_sub(row0(ew[1], 2), I2());
+    wait_vmcnt<0>();
+    __syncthreads();
+    f32x16_t sc = zero16(), pc = zero16();
+#pragma unroll
+    for (int dk = 0; dk < NDK; ++dk) {
+      sc = mfma32(rfrag(ks0, dk), qf[dk], sc);
+      pc = mfma32(rfrag(vs0, dk), gf[dk], pc);
+    }
+    if (!plan_full(e0)) mask(sc, row0(e0, 0), kd0);
+
+    auto body = [&](auto Rc, int u) {
+      constexpr int R = decltype(Rc)::value;
+      using IR = std::integral_constant<int, R>;
+      using IR1 = std::integral_constant<int, (R + 1) % 4>;
+      using IR3 = std::integral_constant<int, (R + 3) % 4>;
+      const int e1 = __builtin_amdgcn_readfirstlane(ew[0]);
+      const int e3 = __builtin_amdgcn_readfirstlane(ew[2]);
+      const int e4 = entry(u + 5);
+      __builtin_amdgcn_sched_barrier(0);
+      dma_sub(row0(e3, u + 3), IR3());
+      bf16x8_t ka[NDK], va[NDK];
+#pragma unroll
+      for (int dk = 0; dk < NDK; ++dk) {
+        ka[dk] = rfrag(kslot(IR1()), dk);
+        va[dk] = rfrag(vslot(IR1()), dk);
+      }
+      f32x16_t sn = zero16(), pn = zero16();
+      bf16x8_t dsf[2];
+      __builtin_amdgcn_sched_barrier(0);
+      constexpr int JPS = 16 / NDK;
+#pragma unroll
+      for (int dk = 0; dk < NDK; ++dk) {
+        sn = mfma32(ka[dk], qf[dk], sn);
+        pn = mfma32(va[dk], gf[dk], pn);
+#pragma unroll
+        for (int j = dk * JPS; j < (dk + 1) * JPS; j += 2) ds2(j, sc, pc, dsf);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // dQ^T += K^T dS^T (A = K^T: column fragments of the K tile).
+#pragma unroll
+      for (int f = 0; f < NVF; ++f)
+        dq_acc[f % NDB] = mfma32(cfrag(kslot(IR()), f), dsf[f / NDB], dq_acc[f % NDB]);
+      sc = sn;
+      pc = pn;
+      if (!plan_full(e1)) mask(sc, row0(e1, u + 1), dslot(IR1()));
+      wait_vmcnt<2 * NDMA>();
+      block_sync_nofence();
+      ew[0] = ew[1];
+      ew[1] = ew[2];
+      ew[2] = ew[3];
+      ew[3] = e4;
+    };
+    int u = 0;
+    for (; u + 4 < U; u += 4) {
+      body(I0(), u);
+      body(I1(), u + 1);
+      body(I2(), u + 2);
+      body(I3(), u + 3);
+    }
+    if (u + 1 < U) { body(I0(), u); ++u; }
+    if (u + 1 < U) { body(I1(), u); ++u; }
+    if (u + 1 < U) { body(I2(), u); ++u; }
+    wait_vmcnt<0>();
+    const int rl = u & 3;
+    const char *kt = rl == 0 ? ks0 : rl == 1 ? ks1 : rl == 2 ? ks2 : ks3;
+    bf16x8_t dsf[2];
+#pragma unroll
+    for (int j = 0; j < 16; j += 2) ds2(j, sc, pc, dsf);
+#pragma unroll
+    for (int f = 0; f < NVF; ++f)
+      dq_acc[f % NDB] = mfma32(cfrag(kt, f), dsf[f / NDB], dq_acc[f % NDB]);
+  }
+
+  if (!qvalid) return;
+  bf16_t *qrow = a.dq.row(b, h, qi);
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int jq = 0; jq < 4; ++jq) {
+      typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+      bf16x4_t o4;
+#pragma unroll
+      for (int x = 0; x < 4; ++x) o4[x] = (bf16_t)(dq_acc[db][4 * jq + x] * a.scale);
+      *reinterpret_cast<bf16x4_t *>(qrow + 32 * db + 8 * jq + 4 * hh) = o4;
+    }
+}
+
 // Two entry points over one body: two waves per SIMD (so one wave's softmax
 // overlaps the other's MFMAs) wherever the registers fit without spilling.
 template <int DP, int WAVES>
@@ -789,15 +1033,22 @@ extern "C" int pb_attn_bwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v,
 #define PB_KV(DP, W, SP) hipLaunchKernelGGL((attn_bwd_dkdv<DP, W, SP>), g_kv, dim3(64 * W), 0, st, a)
 #define PB_BY_D(M, ...) \
   do { if (d <= 32) M(32, __VA_ARGS__); else if (d <= 64) M(64, __VA_ARGS__); else M(128, __VA_ARGS__); } while (0)
-  if (cfg.dq_waves == 4) PB_BY_D(PB_DQ, 4); else PB_BY_D(PB_DQ, 2);
-  rc = launch_status("pb_attn_bwd(dq)");
-  if (rc) return rc;
-  // DMA-pipelined dK/dV where views, documents and the sequence length allow.
+  // DMA-pipelined kernels where views, documents and the sequence length allow.
   const bool pipe = a.vec && (d == 64 || d == 128) && s % 64 == 0 &&
                     (reinterpret_cast<uintptr_t>(doc_ids) & 15) == 0 && doc_stride % 2 == 0 &&
                     (reinterpret_cast<uintptr_t>(lse) & 15) == 0 &&
                     (reinterpret_cast<uintptr_t>(workspace) & 15) == 0 &&
-                    32 * std::max(q->stride_s, dout->stride_s) < (1LL << 30);
+                    32 * std::max({q->stride_s, dout->stride_s, k->stride_s, v->stride_s}) <
+                        (1LL << 30);
+  if (pipe) {
+#define PB_DQP(DP, W) hipLaunchKernelGGL((attn_bwd_dq_pipe<DP, W>), g_q, dim3(64 * W), 0, st, a)
+    if (cfg.dq_waves == 4) { if (d == 128) PB_DQP(128, 4); else PB_DQP(64, 4); }
+    else { if (d == 128) PB_DQP(128, 2); else PB_DQP(64, 2); }
+#undef PB_DQP
+  } else if (cfg.dq_waves == 4) PB_BY_D(PB_DQ, 4);
+  else PB_BY_D(PB_DQ, 2);
+  rc = launch_status("pb_attn_bwd(dq)");
+  if (rc) return rc;
   if (pipe) {
 #define PB_KVP(DP, W, SP) \
   hipLaunchKernelGGL((attn_bwd_dkdv_pipe<DP, W, SP>), g_kv, dim3(64 * W), 0, st, a)
