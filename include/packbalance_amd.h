@@ -203,6 +203,19 @@ int pb_lmhead_ce_bwd(const void *x, int64_t ldx, const void *w, int64_t ldw, con
                      int64_t vchunk, void *workspace, void *dx, int dx_dtype, int64_t lddx,
                      void *dw, int dw_dtype, int64_t lddw, void *stream);
 
+/* ---- Rotary position embedding (q and k in one launch) ------------------
+ * Replaces packbalance/model/rope.py:34-42 (apply_rotary_pos_emb, NeoX
+ * rotate_half).  q [b, hq, s, d] and k [b, hkv, s, d] are pb_bhsd views with
+ * a contiguous head dim (d even); q_out / k_out may alias q / k.  cos and
+ * sin are fp32 [b, s, d/2] (already gathered by position id, rope.py:26) with
+ * a contiguous last dim and the given b / s strides.  inverse = 0 rotates by
+ * +theta (forward), inverse = 1 by -theta (the backward of the forward).
+ * Arithmetic is fp32 with one rounding to dtype.                            */
+int pb_rope_qk(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *q_out, const pb_bhsd *k_out,
+               const float *cos, int64_t cos_stride_b, int64_t cos_stride_s, const float *sin,
+               int64_t sin_stride_b, int64_t sin_stride_s, int64_t b, int64_t s, int64_t hq,
+               int64_t hkv, int64_t d, int dtype, int inverse, void *stream);
+
 /* Layout helper of the CE path: dst (bf16) <- src (any float dtype), cast
  * and, if transpose, transposed; dst is [dst_rows, dst_cols] with row stride
  * dst_ld, and every dst element outside the copied [rows, cols] (or

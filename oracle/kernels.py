@@ -1,4 +1,4 @@
-"""CPU restatement of PackBalance's RMSNorm / SwiGLU / cross-entropy (test oracle).
+"""CPU restatement of PackBalance's RMSNorm / SwiGLU / cross-entropy / RoPE (test oracle).
 
 All math runs in float64 on the CPU unless a caller asks otherwise.  Inputs
 are taken as given (a bf16 tensor is first widened exactly to float64), so the
@@ -127,3 +127,22 @@ def full_ce_reference(x: torch.Tensor, w: torch.Tensor, targets: torch.Tensor,
         valid = targets != -100
         loss = loss + z_loss_coeff * (lse[valid] ** 2).sum()
     return loss
+
+
+# ---------------------------------------------------------------- RoPE
+def rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, *, inverse: bool = False):
+    """apply_rotary_pos_emb of reference ``model/rope.py:29-42`` for one tensor, float64.
+
+    x [B, H, S, D]; cos, sin [B, S, D/2] (already gathered by position id, rope.py:26).
+    With x = [x1, x2] split at D/2: out1 = x1*c - x2*s, out2 = x2*c + x1*s, i.e.
+    x*cat(c, c) + rotate_half(x)*cat(s, s) (rotate_half(x) = [-x2, x1], rope.py:29-31).
+    inverse=True rotates by -theta (s -> -s): the backward of the forward.
+    """
+    xf = _f64(x)
+    c = _f64(cos)[:, None]
+    s = _f64(sin)[:, None]
+    if inverse:
+        s = -s
+    half = xf.shape[-1] // 2
+    x1, x2 = xf[..., :half], xf[..., half:]
+    return torch.cat((x1 * c - x2 * s, x2 * c + x1 * s), dim=-1)

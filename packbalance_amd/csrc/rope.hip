@@ -1,0 +1,166 @@
+// Rotary position embedding (NeoX rotate_half) applied to q and k in one
+// launch, forward and backward, for gfx950.
+//
+// Reference semantics: packbalance/model/rope.py:34-42.  With x = [x1, x2]
+// split at D/2 and c, s = cos, sin of the row's position (fp32 [B, S, D/2],
+// already gathered by position id as rope.py:26 does):
+//   forward   out1 = x1*c - x2*s,   out2 = x2*c + x1*s
+//   backward  dx1  = g1*c + g2*s,   dx2  = g2*c - g1*s     (rotation by -theta)
+// The reference rounds cos/sin, both products and the sum to q's dtype; here
+// the arithmetic is fp32 and the result is rounded once.
+//
+// Rows are (pack, position, head) with the head fastest, so consecutive rows
+// share cos/sin and, for the model's [B, S, H, D] memory, are contiguous.
+// Each lane moves 8 elements of each half (two 16-byte loads and stores) and
+// the 8 cos and sin values of that slice; q rows come first, then k rows.
+#include <initializer_list>
+
+#include "common.hpp"
+
+namespace pb {
+namespace {
+
+struct RopeTensor {
+  const void *x;
+  void *out;
+  int64_t xsb, xsh, xss;  // element strides of x (inner dim contiguous)
+  int64_t osb, osh, oss;  // element strides of out
+  int64_t heads;
+};
+
+struct RopeArgs {
+  RopeTensor t[2];  // q, k
+  const float *cos, *sin;
+  int64_t csb, css, ssb, sss;  // element strides of cos / sin ([B, S, D/2])
+  int64_t S, rows_q, rows;     // rows_q = B*S*Hq, rows = rows_q + B*S*Hkv
+  int half;                    // D / 2
+};
+
+template <typename T, bool INV>
+__global__ __launch_bounds__(256) void rope_vec(RopeArgs a) {
+  constexpr int VEC = 16 / sizeof(T);
+  const int tpr = a.half / VEC;  // lanes per row
+  const int64_t gt = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = gt / tpr;
+  if (row >= a.rows) return;
+  const int d0 = (int)(gt - row * tpr) * VEC;
+  const bool isk = row >= a.rows_q;
+  const RopeTensor &t = a.t[isk ? 1 : 0];
+  const int64_t r = isk ? row - a.rows_q : row;
+  const int64_t h = r % t.heads, bs = r / t.heads;
+  const int64_t s = bs % a.S, b = bs / a.S;
+  const T *x = static_cast<const T *>(t.x) + b * t.xsb + h * t.xsh + s * t.xss + d0;
+  T *o = static_cast<T *>(t.out) + b * t.osb + h * t.osh + s * t.oss + d0;
+  float x1[VEC], x2[VEC], c[VEC], sn[VEC];
+  load16_nt<T>(x, x1);
+  load16_nt<T>(x + a.half, x2);
+  const float *cp = a.cos + b * a.csb + s * a.css + d0;
+  const float *sp = a.sin + b * a.ssb + s * a.sss + d0;
+#pragma unroll
+  for (int i = 0; i < VEC; i += 4) {
+    const float4 c4 = *reinterpret_cast<const float4 *>(cp + i);
+    const float4 s4 = *reinterpret_cast<const float4 *>(sp + i);
+    c[i] = c4.x; c[i + 1] = c4.y; c[i + 2] = c4.z; c[i + 3] = c4.w;
+    sn[i] = s4.x; sn[i + 1] = s4.y; sn[i + 2] = s4.z; sn[i + 3] = s4.w;
+  }
+  float o1[VEC], o2[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) {
+    const float si = INV ? -sn[i] : sn[i];
+    o1[i] = x1[i] * c[i] - x2[i] * si;
+    o2[i] = x2[i] * c[i] + x1[i] * si;
+  }
+  store16_nt<T>(o, o1);
+  store16_nt<T>(o + a.half, o2);
+}
+
+// Any alignment / odd half-dim: one lane per (row, d < D/2) pair.
+template <typename T, bool INV>
+__global__ __launch_bounds__(256) void rope_scalar(RopeArgs a) {
+  const int64_t gt = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = gt / a.half;
+  if (row >= a.rows) return;
+  const int d = (int)(gt - row * a.half);
+  const bool isk = row >= a.rows_q;
+  const RopeTensor &t = a.t[isk ? 1 : 0];
+  const int64_t r = isk ? row - a.rows_q : row;
+  const int64_t h = r % t.heads, bs = r / t.heads;
+  const int64_t s = bs % a.S, b = bs / a.S;
+  const T *x = static_cast<const T *>(t.x) + b * t.xsb + h * t.xsh + s * t.xss;
+  T *o = static_cast<T *>(t.out) + b * t.osb + h * t.osh + s * t.oss;
+  const float c = a.cos[b * a.csb + s * a.css + d];
+  const float si = INV ? -a.sin[b * a.ssb + s * a.sss + d] : a.sin[b * a.ssb + s * a.sss + d];
+  const float x1 = to_f32(x[d]), x2 = to_f32(x[d + a.half]);
+  o[d] = from_f32<T>(x1 * c - x2 * si);
+  o[d + a.half] = from_f32<T>(x2 * c + x1 * si);
+}
+
+bool al16(const void *p, int64_t elem_bytes, std::initializer_list<int64_t> strides) {
+  if (reinterpret_cast<uintptr_t>(p) & 15) return false;
+  for (int64_t st : strides)
+    if ((st * elem_bytes) & 15) return false;
+  return true;
+}
+
+template <typename T>
+int launch(const RopeArgs &a, bool inverse, hipStream_t st) {
+  constexpr int VEC = 16 / sizeof(T);
+  bool vec = a.half % VEC == 0 &&
+             al16(a.cos, 4, {a.csb, a.css}) && al16(a.sin, 4, {a.ssb, a.sss});
+  for (const RopeTensor &t : a.t)
+    vec = vec && al16(t.x, sizeof(T), {t.xsb, t.xsh, t.xss, (int64_t)a.half}) &&
+          al16(t.out, sizeof(T), {t.osb, t.osh, t.oss});
+  if (vec) {
+    const int64_t threads = a.rows * (a.half / VEC);
+    dim3 grid((unsigned)((threads + 255) / 256));
+    if (inverse) hipLaunchKernelGGL((rope_vec<T, true>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((rope_vec<T, false>), grid, dim3(256), 0, st, a);
+  } else {
+    const int64_t threads = a.rows * a.half;
+    dim3 grid((unsigned)((threads + 255) / 256));
+    if (inverse) hipLaunchKernelGGL((rope_scalar<T, true>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((rope_scalar<T, false>), grid, dim3(256), 0, st, a);
+  }
+  return launch_status("pb_rope_qk");
+}
+
+}  // namespace
+}  // namespace pb
+
+extern "C" int pb_rope_qk(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *q_out,
+                          const pb_bhsd *k_out, const float *cos, int64_t cos_stride_b,
+                          int64_t cos_stride_s, const float *sin, int64_t sin_stride_b,
+                          int64_t sin_stride_s, int64_t b, int64_t s, int64_t hq, int64_t hkv,
+                          int64_t d, int dtype, int inverse, void *stream) {
+  using namespace pb;
+  clear_error();
+  PB_CHECK_ARG(valid_dtype(dtype), "pb_rope_qk: bad dtype %d", dtype);
+  PB_CHECK_ARG(q && k && q_out && k_out && cos && sin, "pb_rope_qk: null argument");
+  PB_CHECK_ARG(b >= 0 && s >= 0 && hq >= 1 && hkv >= 1 && d >= 2 && d % 2 == 0,
+               "pb_rope_qk: bad shape b=%lld s=%lld hq=%lld hkv=%lld d=%lld (d must be even)",
+               (long long)b, (long long)s, (long long)hq, (long long)hkv, (long long)d);
+  PB_CHECK_SUPPORTED((b * s * (hq + hkv)) * (d / 2) < (1LL << 40), "pb_rope_qk: problem too large");
+  if (b == 0 || s == 0) return PB_OK;
+  RopeArgs a;
+  const pb_bhsd *in[2] = {q, k}, *out[2] = {q_out, k_out};
+  const int64_t heads[2] = {hq, hkv};
+  for (int i = 0; i < 2; ++i) {
+    a.t[i].x = in[i]->data;
+    a.t[i].out = out[i]->data;
+    a.t[i].xsb = in[i]->stride_b; a.t[i].xsh = in[i]->stride_h; a.t[i].xss = in[i]->stride_s;
+    a.t[i].osb = out[i]->stride_b; a.t[i].osh = out[i]->stride_h; a.t[i].oss = out[i]->stride_s;
+    a.t[i].heads = heads[i];
+  }
+  a.cos = cos; a.sin = sin;
+  a.csb = cos_stride_b; a.css = cos_stride_s; a.ssb = sin_stride_b; a.sss = sin_stride_s;
+  a.S = s;
+  a.rows_q = b * s * hq;
+  a.rows = a.rows_q + b * s * hkv;
+  a.half = (int)(d / 2);
+  hipStream_t st = as_stream(stream);
+  switch (dtype) {
+    case PB_F32: return launch<float>(a, inverse != 0, st);
+    case PB_BF16: return launch<bf16_t>(a, inverse != 0, st);
+    default: return launch<f16_t>(a, inverse != 0, st);
+  }
+}

@@ -1,16 +1,22 @@
-"""Rotary position embeddings with per-document position ids (harness, plain PyTorch).
+"""Rotary position embeddings with per-document position ids.
 
-Same math as the reference ``packbalance/model/rope.py:9-42``: an fp32
-cos/sin cache indexed by per-document ``position_ids``; ``rotate_half``
-(NeoX) applied to q and k in their dtype.  The reference's host-synchronising
-range check (``int(position_ids.max())``, rope.py:21) is left out: the
-harness builds its position ids itself.
+``RotaryEmbedding`` and ``rotate_half`` follow the reference
+``packbalance/model/rope.py:9-31`` (fp32 cos/sin cache indexed by
+per-document ``position_ids``; the reference's host-synchronising range check
+``int(position_ids.max())``, rope.py:21, is left out).  ``apply_rotary_pos_emb``
+keeps the reference signature (rope.py:34-42) and runs the gfx950 kernel
+``pb_rope_qk``: q and k rotated in one launch, fp32 arithmetic with one
+rounding to q's dtype (the reference rounds cos/sin, both products and the
+sum to q's dtype), and the backward as the inverse rotation of the incoming
+gradients.  There is no CPU fallback: CPU tensors raise.
 """
 
 from __future__ import annotations
 
 import torch
 from torch import nn
+
+from packbalance_amd import _native as N
 
 
 class RotaryEmbedding(nn.Module):
@@ -32,7 +38,70 @@ def rotate_half(x: torch.Tensor) -> torch.Tensor:
     return torch.cat((-x[..., half:], x[..., :half]), dim=-1)
 
 
-def apply_rotary_pos_emb(q, k, cos, sin):
-    cos = torch.cat((cos, cos), dim=-1).unsqueeze(1).to(dtype=q.dtype)
-    sin = torch.cat((sin, sin), dim=-1).unsqueeze(1).to(dtype=q.dtype)
-    return (q * cos) + (rotate_half(q) * sin), (k * cos) + (rotate_half(k) * sin)
+def _like(t: torch.Tensor) -> torch.Tensor:
+    """An empty tensor with t's strides (empty_like preserves a dense layout such
+    as the model's [B, S, H, D] memory viewed as [B, H, S, D])."""
+    return torch.empty_like(t)
+
+
+def _head_dim_contiguous(t: torch.Tensor) -> torch.Tensor:
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
+def _cos_sin(c: torch.Tensor, batch: int, seq: int, half: int) -> tuple[torch.Tensor, int, int]:
+    c = c.float()
+    if c.dim() == 2:
+        c = c[None]
+    if c.dim() != 3 or c.shape[1] != seq or c.shape[2] != half or c.shape[0] not in (1, batch):
+        raise ValueError(f"cos/sin shape {tuple(c.shape)} does not match [B={batch}, S={seq}, D/2={half}]")
+    if c.stride(-1) != 1:
+        c = c.contiguous()
+    return c, (c.stride(0) if c.shape[0] == batch else 0), c.stride(1)
+
+
+def _rope(q, k, qo, ko, cos, sin, inverse: int) -> None:
+    b, hq, s, d = q.shape
+    c, csb, css = _cos_sin(cos, b, s, d // 2)
+    sn, ssb, sss = _cos_sin(sin, b, s, d // 2)
+    N.call("pb_rope_qk", N.BHSD.of(q), N.BHSD.of(k), N.BHSD.of(qo), N.BHSD.of(ko),
+           c.data_ptr(), csb, css, sn.data_ptr(), ssb, sss, b, s, hq, k.shape[1], d,
+           N.dtype_code(q), inverse, N.stream_ptr(q))
+
+
+class _RotaryQK(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, cos, sin):
+        N.require_device(q, k, op="apply_rotary_pos_emb")
+        if q.dim() != 4 or k.dim() != 4 or q.shape[0] != k.shape[0] or q.shape[2:] != k.shape[2:]:
+            raise ValueError(f"apply_rotary_pos_emb: q {tuple(q.shape)} / k {tuple(k.shape)} "
+                             "must be [B, H, S, D] with matching B, S, D")
+        if q.shape[-1] % 2:
+            raise ValueError("RoPE requires an even head_dim")
+        q = _head_dim_contiguous(q)
+        k = _head_dim_contiguous(k if k.dtype == q.dtype else k.to(q.dtype))
+        qo, ko = _like(q), _like(k)
+        _rope(q, k, qo, ko, cos, sin, 0)
+        ctx.save_for_backward(cos, sin)
+        ctx.q_shape, ctx.k_shape = q.shape, k.shape
+        return qo, ko
+
+    @staticmethod
+    def backward(ctx, gq, gk):
+        cos, sin = ctx.saved_tensors
+        if gq is None or gk is None:  # only one of q', k' was used
+            ref = gk if gq is None else gq
+            if gq is None:
+                gq = ref.new_zeros(ctx.q_shape).expand(ctx.q_shape)
+            else:
+                gk = ref.new_zeros(ctx.k_shape).expand(ctx.k_shape)
+        gq = _head_dim_contiguous(gq)
+        gk = _head_dim_contiguous(gk if gk.dtype == gq.dtype else gk.to(gq.dtype))
+        dq, dk = _like(gq), _like(gk)
+        _rope(gq, gk, dq, dk, cos, sin, 1)
+        return dq, dk, None, None
+
+
+def apply_rotary_pos_emb(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor,
+                         sin: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """q [B, Hq, S, D], k [B, Hkv, S, D] rotated by cos/sin [B, S, D/2] (gfx950 kernel)."""
+    return _RotaryQK.apply(q, k, cos, sin)

@@ -98,6 +98,56 @@ def test_linear_ce_rejects_row_mismatch() -> None:
 
 
 # ---------------------------------------------------------------- attention
+def _rope_inputs(seed: int = 0, B: int = 2, H: int = 3, S: int = 11, D: int = 16):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(B, H, S, D, generator=g, dtype=torch.float64)
+    theta = torch.rand(B, S, D // 2, generator=g, dtype=torch.float64) * 6.0
+    return x, theta
+
+
+def test_rope_oracle_rotation_invariants() -> None:
+    """rope.py:34-42 rotates each (d, d + D/2) pair: pinned by what a rotation fixes."""
+    x, th = _rope_inputs()
+    c, s = th.cos(), th.sin()
+    y = OK.rope(x, c, s)
+    half = x.shape[-1] // 2
+    # each pair keeps its norm
+    torch.testing.assert_close(y[..., :half] ** 2 + y[..., half:] ** 2,
+                               x[..., :half] ** 2 + x[..., half:] ** 2)
+    # angle 0 is the identity; the inverse undoes the forward
+    torch.testing.assert_close(OK.rope(x, torch.ones_like(c), torch.zeros_like(s)), x)
+    torch.testing.assert_close(OK.rope(y, c, s, inverse=True), x)
+    # angles add: rope(a) then rope(b) == rope(a + b)
+    th2 = _rope_inputs(seed=1)[1]
+    torch.testing.assert_close(OK.rope(y, th2.cos(), th2.sin()), OK.rope(x, (th + th2).cos(), (th + th2).sin()))
+    # a quarter turn maps (x1, x2) -> (-x2, x1), the reference's rotate_half
+    q = OK.rope(x, torch.zeros_like(c), torch.ones_like(s))
+    torch.testing.assert_close(q, torch.cat((-x[..., half:], x[..., :half]), dim=-1))
+
+
+def test_rope_oracle_backward_is_the_adjoint() -> None:
+    """<rope(x), g> == <x, rope_inverse(g)>: the inverse rotation is the exact backward."""
+    x, th = _rope_inputs(seed=2)
+    g = _rope_inputs(seed=3)[0]
+    c, s = th.cos(), th.sin()
+    lhs = (OK.rope(x, c, s) * g).sum()
+    rhs = (x * OK.rope(g, c, s, inverse=True)).sum()
+    assert abs(float(lhs - rhs)) < 1e-10 * float(x.abs().sum() * g.abs().max())
+    # and the transpose of the forward's matrix, column by column on one pair
+    e = torch.zeros(1, 1, 1, 2, dtype=torch.float64)
+    cs, sn = th[:1, :1, :1].cos(), th[:1, :1, :1].sin()
+    cols = []
+    for i in range(2):
+        e.zero_()
+        e[..., i] = 1.0
+        cols.append(OK.rope(e, cs, sn).flatten())
+    m = torch.stack(cols, dim=1)  # forward matrix
+    for i in range(2):
+        e.zero_()
+        e[..., i] = 1.0
+        torch.testing.assert_close(OK.rope(e, cs, sn, inverse=True).flatten(), m.T[:, i])
+
+
 def test_attention_oracle_matches_sdpa_dense_mask() -> None:
     # The reference's eager-attention test pattern (tests/test_attention.py:14-23).
     torch.manual_seed(0)
