@@ -203,6 +203,31 @@ int pb_lmhead_ce_bwd(const void *x, int64_t ldx, const void *w, int64_t ldw, con
                      int64_t vchunk, void *workspace, void *dx, int dx_dtype, int64_t lddx,
                      void *dw, int dw_dtype, int64_t lddw, void *stream);
 
+/* ---- Fused residual add + RMSNorm (per-operand dtypes) ------------------
+ * Replaces the decoder's `hidden = hidden + sublayer_out` followed by the
+ * next rmsnorm (packbalance/model/llama.py:122-125 with
+ * packbalance/kernels/rmsnorm.py:77-125), and the autocast casts around it:
+ *   h = x + delta  (delta may be NULL: h = x),  written to h_out in x_dtype
+ *   (h_out may be NULL or alias x);  y = h * rstd * w in y_dtype;
+ *   rstd[rows] fp32.
+ * Backward (workspace: pb_add_rmsnorm_bwd_workspace_bytes):
+ *   d = rstd*(dy*w - h_hat*mean(dy*w*h_hat)) + dres  (dres may be NULL)
+ *   dx = d in h_dtype, ddelta = d in ddelta_dtype (may be NULL),
+ *   dw = sum_rows dy*h_hat in w_dtype.   dx may alias dres.
+ * Unit inner stride; row strides in elements.                                */
+int pb_add_rmsnorm_fwd(const void *x, int64_t x_row_stride, int x_dtype, const void *delta,
+                       int64_t delta_row_stride, int delta_dtype, void *h_out,
+                       int64_t h_row_stride, const void *w, int w_dtype, void *y,
+                       int64_t y_row_stride, int y_dtype, float *rstd, int64_t rows, int64_t n,
+                       float eps, void *stream);
+int64_t pb_add_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t n);
+int pb_add_rmsnorm_bwd(const void *dy, int64_t dy_row_stride, int dy_dtype, const void *h,
+                       int64_t h_row_stride, int h_dtype, const void *w, int w_dtype,
+                       const float *rstd, const void *dres, int64_t dres_row_stride, void *dx,
+                       int64_t dx_row_stride, void *ddelta, int64_t ddelta_row_stride,
+                       int ddelta_dtype, void *dw, void *workspace, int64_t rows, int64_t n,
+                       void *stream);
+
 /* ---- Rotary position embedding (q and k in one launch) ------------------
  * Replaces packbalance/model/rope.py:34-42 (apply_rotary_pos_emb, NeoX
  * rotate_half).  q [b, hq, s, d] and k [b, hkv, s, d] are pb_bhsd views with

@@ -48,6 +48,24 @@ def rmsnorm_bwd(dy: torch.Tensor, x: torch.Tensor, w: torch.Tensor, eps: float):
     return dx.reshape(xf.shape), dw
 
 
+def add_rmsnorm_fwd(x: torch.Tensor, delta: torch.Tensor, w: torch.Tensor, eps: float):
+    """The decoder's residual add (reference ``model/llama.py:122-125``) followed by the
+    next RMSNorm: h = x + delta; (y, rstd) = rmsnorm_fwd(h).  Returns (h, y, rstd)."""
+    h = _f64(x) + _f64(delta)
+    y, rstd = rmsnorm_fwd(h, w, eps)
+    return h, y, rstd
+
+
+def add_rmsnorm_bwd(dy: torch.Tensor, dres: torch.Tensor | None, h: torch.Tensor,
+                    w: torch.Tensor, eps: float):
+    """Gradients of (h, y) = add_rmsnorm(x, delta): d = rmsnorm dx + dres flows to both
+    x and delta unchanged (the add's Jacobian is the identity).  Returns (d, dw)."""
+    dx, dw = rmsnorm_bwd(dy, h, w, eps)
+    if dres is not None:
+        dx = dx + _f64(dres)
+    return dx, dw
+
+
 # ---------------------------------------------------------------- SwiGLU
 def swiglu_fwd(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     """``silu(g)*u`` -- reference ``kernels/reference.py:16-17``, ``kernels/swiglu.py:28-30``."""

@@ -89,6 +89,17 @@ SIGNATURES: dict[str, tuple] = {
          _i64, _p, _p, _i32, _i64, _p, _i32, _i64, _p],
     ),
     "pb_pack_bf16": (_i32, [_p, _i32, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i32, _p]),
+    "pb_add_rmsnorm_fwd": (
+        _i32,
+        [_p, _i64, _i32, _p, _i64, _i32, _p, _i64, _p, _i32, _p, _i64, _i32, _p, _i64, _i64, _f32,
+         _p],
+    ),
+    "pb_add_rmsnorm_bwd_workspace_bytes": (_i64, [_i64, _i64]),
+    "pb_add_rmsnorm_bwd": (
+        _i32,
+        [_p, _i64, _i32, _p, _i64, _i32, _p, _i32, _p, _p, _i64, _p, _i64, _p, _i64, _i32, _p, _p,
+         _i64, _i64, _p],
+    ),
     "pb_rope_qk": (
         _i32,
         [_pv, _pv, _pv, _pv, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32,

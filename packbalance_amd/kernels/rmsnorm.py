@@ -82,3 +82,123 @@ class _RMSNorm(torch.autograd.Function):
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     """``x * rsqrt(mean(x^2) + eps) * weight`` with fp32 statistics (gfx950 kernel)."""
     return _RMSNorm.apply(x, weight, eps)
+
+
+# ---------------------------------------------------------------- fused residual add
+def _fwd_call(x2d, d2d, h, w, y, rstd, eps):
+    rows, n = x2d.shape
+    N.call(
+        "pb_add_rmsnorm_fwd",
+        x2d.data_ptr(), x2d.stride(0), N.dtype_code(x2d),
+        d2d.data_ptr() if d2d is not None else None, d2d.stride(0) if d2d is not None else n,
+        N.dtype_code(d2d) if d2d is not None else N.dtype_code(x2d),
+        h.data_ptr() if h is not None else None, h.stride(0) if h is not None else n,
+        w.data_ptr(), N.dtype_code(w),
+        y.data_ptr(), y.stride(0), N.dtype_code(y),
+        rstd.data_ptr(), rows, n, float(eps), N.stream_ptr(x2d),
+    )
+
+
+def _bwd_call(dy2d, h2d, w, rstd, dres, dx, ddelta, dw):
+    rows, n = h2d.shape
+    ws_bytes = N.lib().pb_add_rmsnorm_bwd_workspace_bytes(rows, n)
+    ws = torch.empty(max(1, ws_bytes // 4), dtype=torch.float32, device=h2d.device)
+    N.call(
+        "pb_add_rmsnorm_bwd",
+        dy2d.data_ptr(), dy2d.stride(0), N.dtype_code(dy2d),
+        h2d.data_ptr(), h2d.stride(0), N.dtype_code(h2d),
+        w.data_ptr(), N.dtype_code(w), rstd.data_ptr(),
+        dres.data_ptr() if dres is not None else None, dres.stride(0) if dres is not None else n,
+        dx.data_ptr(), dx.stride(0),
+        ddelta.data_ptr() if ddelta is not None else None,
+        ddelta.stride(0) if ddelta is not None else n,
+        N.dtype_code(ddelta) if ddelta is not None else N.dtype_code(dx),
+        dw.data_ptr(), ws.data_ptr(), rows, n, N.stream_ptr(h2d),
+    )
+
+
+def _check(x, weight, op):
+    N.require_device(x, weight, op=op)
+    n = x.shape[-1]
+    if weight.dim() != 1 or weight.shape[0] != n:
+        raise ValueError(f"{op}: weight shape {tuple(weight.shape)} does not match ({n},)")
+    if n > _MAX_N:
+        raise RuntimeError("RMSNorm feature dimension is too large for this kernel")
+
+
+class _AddRMSNorm(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, delta, weight, eps, out_dtype):
+        _check(x, weight, "add_rmsnorm")
+        if delta.shape != x.shape:
+            raise ValueError(f"add_rmsnorm: delta {tuple(delta.shape)} and x {tuple(x.shape)} differ")
+        x2d, d2d, w = _rows(x), _rows(delta), weight.contiguous()
+        rows, n = x2d.shape
+        h = torch.empty((rows, n), dtype=x.dtype, device=x.device)
+        y = torch.empty((rows, n), dtype=out_dtype, device=x.device)
+        rstd = torch.empty(rows, dtype=torch.float32, device=x.device)
+        _fwd_call(x2d, d2d, h, w, y, rstd, eps)
+        ctx.save_for_backward(h, w, rstd)
+        ctx.meta = (x.shape, delta.dtype, weight.dtype)
+        return h.reshape(x.shape), y.reshape(x.shape)
+
+    @staticmethod
+    def backward(ctx, dh, dy):
+        h, w, rstd = ctx.saved_tensors
+        shape, delta_dtype, w_dtype = ctx.meta
+        rows, n = h.shape
+        dy2d = _rows(dy) if dy is not None else torch.zeros_like(h)
+        dres = None
+        if dh is not None:
+            dres = _rows(dh)
+            dres = dres if dres.dtype == h.dtype else dres.to(h.dtype)
+        dx = torch.empty_like(h)
+        ddelta = torch.empty((rows, n), dtype=delta_dtype, device=h.device)
+        dw = torch.empty(n, dtype=w.dtype, device=w.device)
+        _bwd_call(dy2d, h, w, rstd, dres, dx, ddelta, dw)
+        return dx.reshape(shape), ddelta.reshape(shape), dw.to(w_dtype), None, None
+
+
+class _RMSNormTo(torch.autograd.Function):
+    """RMSNorm whose output dtype differs from the input's (no residual add)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, eps, out_dtype):
+        _check(x, weight, "rmsnorm")
+        x2d, w = _rows(x), weight.contiguous()
+        rows, n = x2d.shape
+        y = torch.empty((rows, n), dtype=out_dtype, device=x.device)
+        rstd = torch.empty(rows, dtype=torch.float32, device=x.device)
+        _fwd_call(x2d, None, None, w, y, rstd, eps)
+        ctx.save_for_backward(x2d, w, rstd)
+        ctx.meta = (x.shape, weight.dtype)
+        return y.reshape(x.shape)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2d, w, rstd = ctx.saved_tensors
+        shape, w_dtype = ctx.meta
+        dx = torch.empty_like(x2d)
+        dw = torch.empty(x2d.shape[1], dtype=w.dtype, device=w.device)
+        _bwd_call(_rows(dy), x2d, w, rstd, None, dx, None, dw)
+        return dx.reshape(shape), dw.to(w_dtype), None, None
+
+
+def add_rmsnorm(x: torch.Tensor, delta: torch.Tensor, weight: torch.Tensor, eps: float,
+                out_dtype: torch.dtype | None = None):
+    """Residual add fused with the next RMSNorm (gfx950 kernel).
+
+    Returns ``(h, y)``: ``h = x + delta`` in x's dtype (the new residual stream) and
+    ``y = rmsnorm(h, weight, eps)`` in ``out_dtype`` (default x's dtype).  The backward
+    takes the gradients of both outputs and returns them summed into ``dx`` (x's dtype)
+    and ``ddelta`` (delta's dtype), so no separate add or cast kernels run.
+    """
+    return _AddRMSNorm.apply(x, delta, weight, eps, out_dtype or x.dtype)
+
+
+def rmsnorm_to(x: torch.Tensor, weight: torch.Tensor, eps: float,
+               out_dtype: torch.dtype) -> torch.Tensor:
+    """``rmsnorm`` written directly in ``out_dtype`` (e.g. fp32 residual -> bf16 activations)."""
+    if out_dtype == x.dtype:
+        return rmsnorm(x, weight, eps)
+    return _RMSNormTo.apply(x, weight, eps, out_dtype)

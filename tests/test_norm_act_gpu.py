@@ -167,3 +167,54 @@ def test_swiglu_cfg5_full_size(dev) -> None:
 def test_swiglu_rejects_cpu() -> None:
     with pytest.raises(RuntimeError):
         swiglu(torch.randn(4), torch.randn(4))
+
+
+# ---------------------------------------------------------------- fused residual add + RMSNorm
+@pytest.mark.parametrize(
+    "rows,n,xdt,ddt,ydt,wdt",
+    [
+        (2048, 768, torch.float32, torch.bfloat16, torch.bfloat16, torch.float32),  # cfg2 flow
+        (300, 2048, torch.float32, torch.bfloat16, torch.bfloat16, torch.float32),  # 4 vectors/lane
+        (64, 512, torch.bfloat16, torch.bfloat16, torch.bfloat16, torch.bfloat16),
+        (40, 4096, torch.float32, torch.float32, torch.bfloat16, torch.float32),  # loop kernel
+        (37, 100, torch.float32, torch.float16, torch.float32, torch.float32),  # n % 8 != 0
+    ],
+)
+def test_add_rmsnorm_matches_oracle(rows, n, xdt, ddt, ydt, wdt, dev) -> None:
+    from packbalance_amd.kernels.rmsnorm import add_rmsnorm
+
+    g = torch.Generator().manual_seed(rows + n)
+    x = torch.randn(rows, n, generator=g).to(dev, xdt)
+    d = torch.randn(rows, n, generator=g).to(dev, ddt)
+    w = (torch.randn(n, generator=g) * 0.1 + 1.0).to(dev, wdt)
+    dy = torch.randn(rows, n, generator=g).to(dev, ydt)
+    dres = torch.randn(rows, n, generator=g).to(dev, xdt)
+    xr, dr, wr = (t.clone().requires_grad_(True) for t in (x, d, w))
+    h, y = add_rmsnorm(xr, dr, wr, 1e-5, out_dtype=ydt)
+    assert h.dtype == xdt and y.dtype == ydt
+    torch.autograd.backward((h, y), (dres, dy))
+    h_ref, y_ref, _ = OK.add_rmsnorm_fwd(x, d, w, 1e-5)
+    gx_ref, gw_ref = OK.add_rmsnorm_bwd(dy, dres, h_ref, w, 1e-5)
+    _close(h, h_ref, TOL[xdt], "h")
+    _close(y, y_ref, TOL[ydt], "y")
+    _close(xr.grad, gx_ref, TOL[xdt] if xdt == torch.float32 else 2e-2, "dx")
+    _close(dr.grad, gx_ref, TOL[ddt], "ddelta")
+    assert xr.grad.dtype == xdt and dr.grad.dtype == ddt and wr.grad.dtype == wdt
+    _close(wr.grad, gw_ref, max(TOL[ydt], 1e-4) * 10, "dw")
+
+
+def test_rmsnorm_to_bf16_matches_oracle(dev) -> None:
+    """fp32 residual in, bf16 activations out (the model's first norm); dx back in fp32."""
+    from packbalance_amd.kernels.rmsnorm import rmsnorm_to
+
+    x, w, _ = _rms_case((512, 768), torch.float32, torch.float32, dev, seed=3)
+    dy = torch.randn(512, 768, device=dev).to(torch.bfloat16)
+    xr, wr = x.clone().requires_grad_(True), w.clone().requires_grad_(True)
+    y = rmsnorm_to(xr, wr, 1e-5, torch.bfloat16)
+    assert y.dtype == torch.bfloat16
+    y.backward(dy)
+    y_ref, _ = OK.rmsnorm_fwd(x, w, 1e-5)
+    dx_ref, dw_ref = OK.rmsnorm_bwd(dy, x, w, 1e-5)
+    _close(y, y_ref, 1e-2, "y")
+    _close(xr.grad, dx_ref, 1e-5, "dx")
+    _close(wr.grad, dw_ref, 1e-4, "dw")

@@ -45,6 +45,26 @@ def test_rmsnorm_oracle_matches_autograd_and_closed_form() -> None:
 
 
 # ---------------------------------------------------------------- SwiGLU
+def test_add_rmsnorm_oracle_matches_autograd() -> None:
+    """h = x + delta then RMSNorm: both outputs' gradients reach x and delta summed."""
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(6, 24, generator=g, dtype=torch.float64, requires_grad=True)
+    d = torch.randn(6, 24, generator=g, dtype=torch.float64, requires_grad=True)
+    w = torch.randn(24, generator=g, dtype=torch.float64, requires_grad=True)
+    dy = torch.randn(6, 24, generator=g, dtype=torch.float64)
+    dres = torch.randn(6, 24, generator=g, dtype=torch.float64)
+    h = x + d
+    y = h * torch.rsqrt((h * h).mean(-1, keepdim=True) + 1e-5) * w
+    torch.autograd.backward((h, y), (dres, dy))
+    oh, oy, _ = OK.add_rmsnorm_fwd(x, d, w, 1e-5)
+    torch.testing.assert_close(oh, h.detach())
+    torch.testing.assert_close(oy, y.detach())
+    ddx, ddw = OK.add_rmsnorm_bwd(dy, dres, oh, w, 1e-5)
+    torch.testing.assert_close(ddx, x.grad)
+    torch.testing.assert_close(ddx, d.grad)
+    torch.testing.assert_close(ddw, w.grad)
+
+
 def test_swiglu_oracle_matches_autograd() -> None:
     torch.manual_seed(0)
     g = torch.randn(8, 16, dtype=torch.float64, requires_grad=True)
