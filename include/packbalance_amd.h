@@ -78,6 +78,23 @@ int pb_swiglu_fwd(const void *gate, const void *up, void *out, int64_t n,
 int pb_swiglu_bwd(const void *gate, const void *up, const void *dy,
                   void *dgate, void *dup, int64_t n, int dtype, void *stream);
 
+/* Row-strided forms of the two above (same math): every operand is a
+ * [rows, cols] block with its own row stride (elements) and unit column
+ * stride, so gate/up may be the two halves of one fused [rows, 2*cols]
+ * projection and dgate/dup may be written back into one such buffer.
+ * Replaces the same reference functions (swiglu.py:23-46), which reach
+ * them through .contiguous() copies of non-contiguous gate/up.              */
+int pb_swiglu_fwd_rows(const void *gate, int64_t gate_row_stride,
+                       const void *up, int64_t up_row_stride, void *out,
+                       int64_t out_row_stride, int64_t rows, int64_t cols,
+                       int dtype, void *stream);
+int pb_swiglu_bwd_rows(const void *gate, int64_t gate_row_stride,
+                       const void *up, int64_t up_row_stride, const void *dy,
+                       int64_t dy_row_stride, void *dgate,
+                       int64_t dgate_row_stride, void *dup,
+                       int64_t dup_row_stride, int64_t rows, int64_t cols,
+                       int dtype, void *stream);
+
 /* ---- Row cross-entropy over a materialised logits block ----------------
  * Replaces packbalance/kernels/fused_ce.py:31-89 (_ce_kernel) and
  * _ce_launch (fused_ce.py:91-118).  Per row r of logits[m, v] (any strides):
@@ -190,7 +207,9 @@ int pb_lmhead_ce_fwd(const void *x, int64_t ldx, const void *w, int64_t ldw, int
  * chunk (vchunk rows of w, a multiple of 8):
  *   dL = (softmax*(1 + 2z*lse) - onehot) * grad_out   (bf16, one chunk)
  *   dx = sum over chunks dL w_chunk   (fp32 accumulation; dx in dx_dtype)
- *   dw[chunk] = dL^T x                (written in dw_dtype)
+ *   dw[chunk] = dL^T x                (written in dw_dtype; with
+ *                                      dw_accumulate != 0, dw must be fp32
+ *                                      and the product is added to it)
  * xt = x^T [d, >= n] and wt = w^T [d, >= v] (bf16, e.g. from pb_pack_bf16);
  * workspace: pb_lmhead_ce_bwd_workspace_bytes(n, v, d, vchunk) bytes (the
  * dlogits chunk in both layouts and fp32 dx accumulators).
@@ -201,7 +220,8 @@ int pb_lmhead_ce_bwd(const void *x, int64_t ldx, const void *w, int64_t ldw, con
                      int64_t d, const int64_t *targets, int64_t ignore_index,
                      float z_loss_coeff, const float *lse, const float *grad_out,
                      int64_t vchunk, void *workspace, void *dx, int dx_dtype, int64_t lddx,
-                     void *dw, int dw_dtype, int64_t lddw, void *stream);
+                     void *dw, int dw_dtype, int64_t lddw, int dw_accumulate,
+                     void *stream);
 
 /* ---- Fused residual add + RMSNorm (per-operand dtypes) ------------------
  * Replaces the decoder's `hidden = hidden + sublayer_out` followed by the

@@ -62,6 +62,9 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "pb_swiglu_fwd": (_i32, [_p, _p, _p, _i64, _i32, _p]),
     "pb_swiglu_bwd": (_i32, [_p, _p, _p, _p, _p, _i64, _i32, _p]),
+    "pb_swiglu_fwd_rows": (_i32, [_p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i32, _p]),
+    "pb_swiglu_bwd_rows": (_i32, [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _i64,
+                                  _i32, _p]),
     "pb_ce_rows": (_i32, [_p, _i64, _i64, _i32, _p, _p, _p, _p, _i64, _i64, _i64, _f32, _p]),
     "pb_doc_block_tables": (
         _i32,
@@ -86,7 +89,7 @@ SIGNATURES: dict[str, tuple] = {
     "pb_lmhead_ce_bwd": (
         _i32,
         [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _p, _i64, _f32, _p, _p,
-         _i64, _p, _p, _i32, _i64, _p, _i32, _i64, _p],
+         _i64, _p, _p, _i32, _i64, _p, _i32, _i64, _i32, _p],
     ),
     "pb_pack_bf16": (_i32, [_p, _i32, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i32, _p]),
     "pb_add_rmsnorm_fwd": (

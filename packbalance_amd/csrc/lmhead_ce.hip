@@ -16,7 +16,7 @@
 //   kDlogits  same product over one vocab chunk; writes dlogits (scaled by the
 //             device-resident grad_output) as dL [tokens][chunk] and dL^T.
 //   kAccum    dx += dL W_chunk (fp32 accumulator; the last chunk writes x's dtype).
-//   kStore    dW_chunk = dL^T x (written in W's dtype).
+//   kStore    dW_chunk = dL^T x (written in W's dtype, or added to an fp32 dW).
 // A small kernel merges the forward partials into lse / per-row loss, and a
 // single workgroup sums the rows in a fixed order (deterministic scalar).
 #include <math.h>
@@ -57,6 +57,7 @@ struct GemmArgs {
   int64_t ldc, ldo;
   int out_dtype;
   int first, last;
+  int accum_out;  // kStore: out is fp32 and the product is added to it
   // kAccum split-K: blockIdx.y = split; each split covers k_per_split of K and
   // writes fp32 partials part[split][M][N]; split_reduce folds them.
   int k_per_split;
@@ -271,6 +272,10 @@ __global__ __launch_bounds__(256) void gemm_nt(GemmArgs g) {
             else
               *p = v;
           } else {
+            if (MODE == kStore && g.accum_out) {
+              static_cast<float *>(g.out)[(int64_t)m * g.ldo + n] += v;
+              continue;
+            }
             store_out(g.out, g.out_dtype, (int64_t)m * g.ldo + n, v);
           }
         }
@@ -520,7 +525,7 @@ extern "C" int pb_lmhead_ce_bwd(const void *x, int64_t ldx, const void *w, int64
                                 int64_t ignore_index, float z_loss_coeff, const float *lse,
                                 const float *grad_out, int64_t vchunk, void *workspace, void *dx,
                                 int dx_dtype, int64_t lddx, void *dw, int dw_dtype, int64_t lddw,
-                                void *stream) {
+                                int dw_accumulate, void *stream) {
   using namespace pb;
   using namespace pb::ce;
   clear_error();
@@ -529,6 +534,8 @@ extern "C" int pb_lmhead_ce_bwd(const void *x, int64_t ldx, const void *w, int64
                      "pb_lmhead_ce_bwd: too large");
   PB_CHECK_ARG(valid_dtype(dx_dtype) && valid_dtype(dw_dtype), "pb_lmhead_ce_bwd: bad dtype");
   PB_CHECK_ARG(vchunk % 8 == 0, "pb_lmhead_ce_bwd: vchunk must be a multiple of 8");
+  PB_CHECK_ARG(!dw_accumulate || dw_dtype == PB_F32,
+               "pb_lmhead_ce_bwd: dw_accumulate needs an fp32 dw");
   PB_CHECK_ARG(k_aligned(x, ldx) && k_aligned(w, ldw) && k_aligned(xt, ldxt) &&
                    k_aligned(wt, ldwt) && k_aligned(workspace, 8) && d % 8 == 0,
                "pb_lmhead_ce_bwd: operands must be 16-byte aligned with row strides %% 8 == 0");
@@ -599,6 +606,7 @@ extern "C" int pb_lmhead_ce_bwd(const void *x, int64_t ldx, const void *w, int64
     gw.out = static_cast<char *>(dw) + v0 * lddw * (dw_dtype == PB_F32 ? 4 : 2);
     gw.ldo = lddw;
     gw.out_dtype = dw_dtype;
+    gw.accum_out = dw_accumulate != 0;
     hipLaunchKernelGGL(gemm_nt<kStore>, dim3(tiles(gw.M, gw.N)), dim3(256), 0, st, gw);
     rc = launch_status("pb_lmhead_ce_bwd(dx/dw)");
     if (rc) return rc;

@@ -7,6 +7,8 @@
 // non-temporal hints (each byte is touched once), several vectors per lane in
 // flight, and the sigmoid runs on the hardware exp2/rcp units so the kernel
 // stays bound by HBM, not by the VALU.
+#include <initializer_list>
+
 #include "common.hpp"
 
 namespace pb {
@@ -183,6 +185,180 @@ int bwd_typed(const void *g, const void *u, const void *d, void *dg, void *du, i
   return launch_status("pb_swiglu_bwd");
 }
 
+
+// Row-strided forms: gate, up, dy and the outputs are [rows][cols] blocks with
+// their own row strides and unit column stride -- e.g. gate and up as the two
+// halves of one fused [rows][2*cols] projection, and dgate/dup written back
+// into one such buffer.  The vector kernels index with 32-bit (row, column)
+// arithmetic; launches hold at most 2^30 vectors.
+template <typename T, int U>
+__global__ __launch_bounds__(kThreads) void swiglu_fwd_rows(const T *__restrict__ gate, int64_t gs,
+                                                            const T *__restrict__ up, int64_t us,
+                                                            T *__restrict__ out, int64_t os,
+                                                            uint32_t cpr, uint32_t nvec) {
+  constexpr int VEC = 16 / sizeof(T);
+  const uint32_t base = blockIdx.x * (uint32_t)(kThreads * U) + threadIdx.x;
+  u32x4 g[U], u[U];
+#pragma unroll
+  for (int k = 0; k < U; ++k) {
+    const uint32_t i = base + (uint32_t)(k * kThreads);
+    if (i < nvec) {
+      const uint32_t r = i / cpr, c = (i - r * cpr) * VEC;
+      g[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(gate + r * gs + c));
+      u[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(up + r * us + c));
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < U; ++k) {
+    const uint32_t i = base + (uint32_t)(k * kThreads);
+    if (i < nvec) {
+      const uint32_t r = i / cpr, c = (i - r * cpr) * VEC;
+      const T *ge = reinterpret_cast<const T *>(&g[k]);
+      const T *ue = reinterpret_cast<const T *>(&u[k]);
+      float y[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float gv = to_f32(ge[e]);
+        y[e] = gv * sigmoid(gv) * to_f32(ue[e]);
+      }
+      store16_nt<T>(out + r * os + c, y);
+    }
+  }
+}
+
+template <typename T, int U>
+__global__ __launch_bounds__(kThreads) void swiglu_bwd_rows(
+    const T *__restrict__ gate, int64_t gs, const T *__restrict__ up, int64_t us,
+    const T *__restrict__ dy, int64_t ds, T *__restrict__ dgate, int64_t dgs, T *__restrict__ dup,
+    int64_t dus, uint32_t cpr, uint32_t nvec) {
+  constexpr int VEC = 16 / sizeof(T);
+  const uint32_t base = blockIdx.x * (uint32_t)(kThreads * U) + threadIdx.x;
+  u32x4 g[U], u[U], d[U];
+#pragma unroll
+  for (int k = 0; k < U; ++k) {
+    const uint32_t i = base + (uint32_t)(k * kThreads);
+    if (i < nvec) {
+      const uint32_t r = i / cpr, c = (i - r * cpr) * VEC;
+      g[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(gate + r * gs + c));
+      u[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(up + r * us + c));
+      d[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(dy + r * ds + c));
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < U; ++k) {
+    const uint32_t i = base + (uint32_t)(k * kThreads);
+    if (i < nvec) {
+      const uint32_t r = i / cpr, c = (i - r * cpr) * VEC;
+      const T *ge = reinterpret_cast<const T *>(&g[k]);
+      const T *ue = reinterpret_cast<const T *>(&u[k]);
+      const T *de = reinterpret_cast<const T *>(&d[k]);
+      float dg[VEC], du[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float gv = to_f32(ge[e]), uv = to_f32(ue[e]), dv = to_f32(de[e]);
+        const float sg = sigmoid(gv);
+        dg[e] = dv * uv * (sg * (1.0f + gv * (1.0f - sg)));
+        du[e] = dv * (gv * sg);
+      }
+      store16_nt<T>(dgate + r * dgs + c, dg);
+      store16_nt<T>(dup + r * dus + c, du);
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void swiglu_fwd_rows_scalar(const T *__restrict__ gate,
+                                                                   int64_t gs,
+                                                                   const T *__restrict__ up,
+                                                                   int64_t us, T *__restrict__ out,
+                                                                   int64_t os, int64_t cols,
+                                                                   int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
+    const int64_t r = i / cols, c = i - r * cols;
+    const float g = to_f32(gate[r * gs + c]);
+    out[r * os + c] = from_f32<T>(g * sigmoid(g) * to_f32(up[r * us + c]));
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void swiglu_bwd_rows_scalar(
+    const T *__restrict__ gate, int64_t gs, const T *__restrict__ up, int64_t us,
+    const T *__restrict__ dy, int64_t ds, T *__restrict__ dgate, int64_t dgs, T *__restrict__ dup,
+    int64_t dus, int64_t cols, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
+    const int64_t r = i / cols, c = i - r * cols;
+    const float g = to_f32(gate[r * gs + c]), u = to_f32(up[r * us + c]), d = to_f32(dy[r * ds + c]);
+    const float s = sigmoid(g);
+    dgate[r * dgs + c] = from_f32<T>(d * u * (s * (1.0f + g * (1.0f - s))));
+    dup[r * dus + c] = from_f32<T>(d * (g * s));
+  }
+}
+
+bool rows_vec_ok(int64_t cols, int64_t elem, std::initializer_list<const void *> ptrs,
+                 std::initializer_list<int64_t> strides) {
+  if ((cols * elem) % 16) return false;
+  for (const void *p : ptrs)
+    if (!aligned16(p)) return false;
+  for (int64_t s : strides)
+    if ((s * elem) % 16) return false;
+  return true;
+}
+
+// Rows per launch so that one launch holds at most 2^30 vectors.
+int64_t rows_per_launch(int64_t cpr) { return cpr >= kMaxVecPerLaunch ? 1 : kMaxVecPerLaunch / cpr; }
+
+template <typename T>
+int fwd_rows_typed(const void *g, int64_t gs, const void *u, int64_t us, void *o, int64_t os,
+                   int64_t rows, int64_t cols, hipStream_t st) {
+  constexpr int VEC = 16 / sizeof(T);
+  const T *G = static_cast<const T *>(g);
+  const T *U = static_cast<const T *>(u);
+  T *O = static_cast<T *>(o);
+  if (rows_vec_ok(cols, sizeof(T), {g, u, o}, {gs, us, os}) && cols / VEC < kMaxVecPerLaunch) {
+    const int64_t cpr = cols / VEC, rpl = rows_per_launch(cpr);
+    for (int64_t r0 = 0; r0 < rows; r0 += rpl) {
+      const int64_t nr = rows - r0 < rpl ? rows - r0 : rpl;
+      const int64_t nv = nr * cpr;
+      hipLaunchKernelGGL((swiglu_fwd_rows<T, kFwdU>), dim3(one_pass_grid(nv, kFwdU)),
+                         dim3(kThreads), 0, st, G + r0 * gs, gs, U + r0 * us, us, O + r0 * os, os,
+                         (uint32_t)cpr, (uint32_t)nv);
+    }
+  } else {
+    hipLaunchKernelGGL((swiglu_fwd_rows_scalar<T>), dim3(grid_for(rows * cols)), dim3(kThreads), 0,
+                       st, G, gs, U, us, O, os, cols, rows * cols);
+  }
+  return launch_status("pb_swiglu_fwd_rows");
+}
+
+template <typename T>
+int bwd_rows_typed(const void *g, int64_t gs, const void *u, int64_t us, const void *d, int64_t ds,
+                   void *dg, int64_t dgs, void *du, int64_t dus, int64_t rows, int64_t cols,
+                   hipStream_t st) {
+  constexpr int VEC = 16 / sizeof(T);
+  const T *G = static_cast<const T *>(g);
+  const T *U = static_cast<const T *>(u);
+  const T *D = static_cast<const T *>(d);
+  T *DG = static_cast<T *>(dg);
+  T *DU = static_cast<T *>(du);
+  if (rows_vec_ok(cols, sizeof(T), {g, u, d, dg, du}, {gs, us, ds, dgs, dus}) &&
+      cols / VEC < kMaxVecPerLaunch) {
+    const int64_t cpr = cols / VEC, rpl = rows_per_launch(cpr);
+    for (int64_t r0 = 0; r0 < rows; r0 += rpl) {
+      const int64_t nr = rows - r0 < rpl ? rows - r0 : rpl;
+      const int64_t nv = nr * cpr;
+      hipLaunchKernelGGL((swiglu_bwd_rows<T, kBwdU>), dim3(one_pass_grid(nv, kBwdU)),
+                         dim3(kThreads), 0, st, G + r0 * gs, gs, U + r0 * us, us, D + r0 * ds, ds,
+                         DG + r0 * dgs, dgs, DU + r0 * dus, dus, (uint32_t)cpr, (uint32_t)nv);
+    }
+  } else {
+    hipLaunchKernelGGL((swiglu_bwd_rows_scalar<T>), dim3(grid_for(rows * cols)), dim3(kThreads), 0,
+                       st, G, gs, U, us, D, ds, DG, dgs, DU, dus, cols, rows * cols);
+  }
+  return launch_status("pb_swiglu_bwd_rows");
+}
+
 }  // namespace
 }  // namespace pb
 
@@ -213,5 +389,51 @@ extern "C" int pb_swiglu_bwd(const void *gate, const void *up, const void *dy, v
     case PB_F32: return bwd_typed<float>(gate, up, dy, dgate, dup, n, st);
     case PB_BF16: return bwd_typed<bf16_t>(gate, up, dy, dgate, dup, n, st);
     default: return bwd_typed<f16_t>(gate, up, dy, dgate, dup, n, st);
+  }
+}
+
+extern "C" int pb_swiglu_fwd_rows(const void *gate, int64_t gate_rs, const void *up, int64_t up_rs,
+                                  void *out, int64_t out_rs, int64_t rows, int64_t cols, int dtype,
+                                  void *stream) {
+  using namespace pb;
+  clear_error();
+  PB_CHECK_ARG(valid_dtype(dtype), "pb_swiglu_fwd_rows: bad dtype %d", dtype);
+  PB_CHECK_ARG(rows >= 0 && cols >= 0, "pb_swiglu_fwd_rows: negative size");
+  if (rows == 0 || cols == 0) return PB_OK;
+  PB_CHECK_ARG(gate && up && out, "pb_swiglu_fwd_rows: null pointer");
+  PB_CHECK_ARG(gate_rs >= cols && up_rs >= cols && out_rs >= cols,
+               "pb_swiglu_fwd_rows: row strides must be >= cols");
+  hipStream_t st = as_stream(stream);
+  switch (dtype) {
+    case PB_F32: return fwd_rows_typed<float>(gate, gate_rs, up, up_rs, out, out_rs, rows, cols, st);
+    case PB_BF16: return fwd_rows_typed<bf16_t>(gate, gate_rs, up, up_rs, out, out_rs, rows, cols, st);
+    default: return fwd_rows_typed<f16_t>(gate, gate_rs, up, up_rs, out, out_rs, rows, cols, st);
+  }
+}
+
+extern "C" int pb_swiglu_bwd_rows(const void *gate, int64_t gate_rs, const void *up, int64_t up_rs,
+                                  const void *dy, int64_t dy_rs, void *dgate, int64_t dgate_rs,
+                                  void *dup, int64_t dup_rs, int64_t rows, int64_t cols, int dtype,
+                                  void *stream) {
+  using namespace pb;
+  clear_error();
+  PB_CHECK_ARG(valid_dtype(dtype), "pb_swiglu_bwd_rows: bad dtype %d", dtype);
+  PB_CHECK_ARG(rows >= 0 && cols >= 0, "pb_swiglu_bwd_rows: negative size");
+  if (rows == 0 || cols == 0) return PB_OK;
+  PB_CHECK_ARG(gate && up && dy && dgate && dup, "pb_swiglu_bwd_rows: null pointer");
+  PB_CHECK_ARG(gate_rs >= cols && up_rs >= cols && dy_rs >= cols && dgate_rs >= cols &&
+                   dup_rs >= cols,
+               "pb_swiglu_bwd_rows: row strides must be >= cols");
+  hipStream_t st = as_stream(stream);
+  switch (dtype) {
+    case PB_F32:
+      return bwd_rows_typed<float>(gate, gate_rs, up, up_rs, dy, dy_rs, dgate, dgate_rs, dup,
+                                   dup_rs, rows, cols, st);
+    case PB_BF16:
+      return bwd_rows_typed<bf16_t>(gate, gate_rs, up, up_rs, dy, dy_rs, dgate, dgate_rs, dup,
+                                    dup_rs, rows, cols, st);
+    default:
+      return bwd_rows_typed<f16_t>(gate, gate_rs, up, up_rs, dy, dy_rs, dgate, dgate_rs, dup,
+                                   dup_rs, rows, cols, st);
   }
 }

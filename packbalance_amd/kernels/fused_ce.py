@@ -162,11 +162,86 @@ class _FusedLinearCE(torch.autograd.Function):
                xt.data_ptr(), xt.stride(0), wt.data_ptr(), wt.stride(0), n, v, d8,
                t.data_ptr(), ctx.ignore_index, ctx.z, lse.data_ptr(), go.data_ptr(), vchunk,
                ws.data_ptr(), dx.data_ptr(), N.dtype_code(dx), dx.stride(0), dw.data_ptr(),
-               N.dtype_code(dw), dw.stride(0), N.stream_ptr(xb))
+               N.dtype_code(dw), dw.stride(0), 0, N.stream_ptr(xb))
         d = ctx.d
         if d8 != d:
             dx, dw = dx[:, :d], dw[:, :d]
         return dx.reshape(ctx.x_shape), dw, None, None, None, None
+
+
+class _LMHeadCEAccum(torch.autograd.Function):
+    """``_FusedLinearCE`` over a caller-held bf16 weight ``wb`` [V, d8] and its transpose
+    ``wt`` [d8, >= V], adding dW (fp32) into ``dw_acc`` instead of returning it."""
+
+    @staticmethod
+    def forward(ctx, x, wb, wt, dw_acc, targets, ignore_index, z_loss_coeff):
+        x2d = x.reshape(-1, x.shape[-1])
+        t = targets.reshape(-1).to(torch.int64).contiguous()
+        n, d = x2d.shape
+        v, d8 = wb.shape
+        if t.shape[0] != n or d8 != _round8(d) or dw_acc.shape[0] != v or dw_acc.shape[1] < d:
+            raise ValueError("lmhead CE: x / weight / targets / dW shapes disagree")
+        if dw_acc.dtype != torch.float32 or dw_acc.stride(1) != 1:
+            raise ValueError("lmhead CE: dW accumulator must be fp32 with unit column stride")
+        dev = x.device
+        total = torch.zeros((), dtype=torch.float32, device=dev)
+        xb = _bf16_rows(x2d)
+        lse = torch.empty(n, dtype=torch.float32, device=dev)
+        rows = torch.empty(n, dtype=torch.float32, device=dev)
+        ws = torch.empty(max(1, N.lib().pb_lmhead_ce_workspace_bytes(n, v) // 4),
+                         dtype=torch.float32, device=dev)
+        N.call("pb_lmhead_ce_fwd", xb.data_ptr(), xb.stride(0), wb.data_ptr(), wb.stride(0),
+               n, v, d8, t.data_ptr(), int(ignore_index), float(z_loss_coeff), rows.data_ptr(),
+               lse.data_ptr(), total.data_ptr(), ws.data_ptr(), N.stream_ptr(x))
+        ctx.save_for_backward(xb, wb, wt, t, lse)
+        ctx.dw_acc, ctx.x_shape, ctx.x_dtype, ctx.d = dw_acc, x.shape, x.dtype, d
+        ctx.ignore_index, ctx.z = int(ignore_index), float(z_loss_coeff)
+        return total
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        xb, wb, wt, t, lse = ctx.saved_tensors
+        n, d8 = xb.shape
+        v = wb.shape[0]
+        dev = xb.device
+        dw = ctx.dw_acc
+        if dw.shape[1] != d8:
+            raise ValueError("lmhead CE: dW accumulator width must equal the padded feature count")
+        xt = _transpose_bf16(xb)
+        vchunk = vocab_chunk(n, v)
+        ws = torch.empty(N.lib().pb_lmhead_ce_bwd_workspace_bytes(n, v, d8, vchunk),
+                         dtype=torch.uint8, device=dev)
+        dx = torch.empty((n, d8), dtype=ctx.x_dtype, device=dev)
+        go = grad_output.detach().to(torch.float32).reshape(1).contiguous()
+        N.call("pb_lmhead_ce_bwd", xb.data_ptr(), xb.stride(0), wb.data_ptr(), wb.stride(0),
+               xt.data_ptr(), xt.stride(0), wt.data_ptr(), wt.stride(0), n, v, d8,
+               t.data_ptr(), ctx.ignore_index, ctx.z, lse.data_ptr(), go.data_ptr(), vchunk,
+               ws.data_ptr(), dx.data_ptr(), N.dtype_code(dx), dx.stride(0), dw.data_ptr(),
+               N.PB_F32, dw.stride(0), 1, N.stream_ptr(xb))
+        if d8 != ctx.d:
+            dx = dx[:, :ctx.d]
+        return dx.reshape(ctx.x_shape), None, None, None, None, None, None
+
+
+def lmhead_weight_bf16(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(wb, wt): ``weight`` as bf16 rows [V, round8(d)] and their transpose [round8(d), round8(V)],
+    to be computed once and passed to ``linear_cross_entropy_accumulate`` while weight is unchanged."""
+    wb = _bf16_rows(weight)
+    return wb, _transpose_bf16(wb)
+
+
+def linear_cross_entropy_accumulate(x: torch.Tensor, wb: torch.Tensor, wt: torch.Tensor,
+                                    dw_acc: torch.Tensor, targets: torch.Tensor,
+                                    *, ignore_index: int = -100,
+                                    z_loss_coeff: float = 0.0) -> torch.Tensor:
+    """``linear_cross_entropy`` for a training loop that owns the weight's bf16 copy.
+
+    The forward and loss are those of ``linear_cross_entropy(x, W)`` with ``(wb, wt) =
+    lmhead_weight_bf16(W)``; the backward returns dx and ADDS dW (fp32) into ``dw_acc``
+    [V, d] (d a multiple of 8) instead of returning it.
+    """
+    N.require_device(x, wb, targets, op="linear_cross_entropy_accumulate")
+    return _LMHeadCEAccum.apply(x, wb, wt, dw_acc, targets, ignore_index, z_loss_coeff)
 
 
 def linear_cross_entropy(

@@ -1,0 +1,170 @@
+"""Flat parameter storage for the training harness: one fp32 buffer for the
+master weights, one for their gradients, and one compute-dtype copy (bf16
+under autocast) of the weights for the matmuls.
+
+Every ``nn.Parameter`` of the model becomes a view into the master buffer
+(``p.data``) and its ``.grad`` a view into the gradient buffer, so
+
+* the step's optimizer and gradient clipping run over ONE tensor (a single
+  ``nn.Parameter`` over the whole master buffer, ``FlatParams.param``);
+* parameters listed as a group (q/k/v, gate/up) are adjacent, so their
+  weights, bf16 copies and gradients are also one ``[sum rows, cols]`` matrix
+  each -- one fused GEMM instead of three or two;
+* matmul backward passes accumulate weight gradients in fp32 straight into
+  the gradient buffer (no bf16 dW, no cast, no separate add per micro-batch).
+
+The compute-dtype copy is what torch's autocast computes on the fly (each
+fp32 weight rounded to bf16 once per autocast region); here it is one cast
+kernel over the whole buffer, run by ``refresh`` -- by the model on every
+forward, or once per step inside ``hold()``.
+"""
+
+from __future__ import annotations
+
+import contextlib
+
+import torch
+from torch import nn
+
+_ALIGN = 64  # elements: every non-grouped parameter and group starts 256-byte aligned
+
+
+def _align(n: int) -> int:
+    return (n + _ALIGN - 1) // _ALIGN * _ALIGN
+
+
+class FlatParams:
+    def __init__(self, model: nn.Module, groups: list[list[nn.Parameter]] = ()) -> None:
+        named = list(model.named_parameters())
+        if not named:
+            raise ValueError("model has no parameters")
+        dev = named[0][1].device
+        follows = {}  # id(param) -> previous member of its group
+        for g in groups:
+            shapes = {tuple(p.shape[1:]) for p in g}
+            if len(shapes) != 1:
+                raise ValueError("grouped parameters must share their trailing shape")
+            for prev, p in zip(g, g[1:]):
+                follows[id(p)] = id(prev)
+        off = 0
+        self._off: dict[int, tuple[int, torch.Size]] = {}
+        last_id = None
+        for _, p in named:
+            if id(p) in follows:
+                if follows[id(p)] != last_id:
+                    raise ValueError("grouped parameters must be registered consecutively")
+            else:
+                off = _align(off)
+            self._off[id(p)] = (off, p.shape)
+            off += p.numel()
+            last_id = id(p)
+        total = _align(off)
+        self.device = dev
+        self.master = torch.zeros(total, dtype=torch.float32, device=dev)
+        self.grad = torch.zeros(total, dtype=torch.float32, device=dev)
+        self._params = [p for _, p in named]
+        with torch.no_grad():
+            for p in self._params:
+                v = self._view(self.master, p)
+                v.copy_(p.detach().float())
+                gv = self._view(self.grad, p)
+                if p.grad is not None:
+                    gv.copy_(p.grad)
+                p.data = v
+                p.grad = gv
+        self._gviews = [p.grad for p in self._params]
+        self.param = nn.Parameter(self.master)
+        self.param.grad = self.grad
+        self._shadow: dict[torch.dtype, torch.Tensor] = {}
+        self._cache: dict[tuple, torch.Tensor] = {}
+        self._held = False
+        self.refreshes = 0  # number of compute-copy refreshes (host-side counter)
+
+    # ------------------------------------------------------------ views
+    def _view(self, buf: torch.Tensor, p: nn.Parameter) -> torch.Tensor:
+        o, shape = self._off[id(p)]
+        return buf[o:o + p.numel()].view(shape)
+
+    def owns(self, model: nn.Module) -> bool:
+        """True while every parameter still lives in this store (no .to(), no re-assign)."""
+        ps = [p for p in model.parameters()]
+        if len(ps) != len(self._params):
+            return False
+        for p in (ps[0], ps[-1]):
+            if id(p) not in self._off or p.data_ptr() != self._view(self.master, p).data_ptr():
+                return False
+        return True
+
+    def _group(self, buf: torch.Tensor, params, key) -> torch.Tensor:
+        ck = (key, tuple(id(p) for p in params))
+        hit = self._cache.get(ck)
+        if hit is not None:
+            return hit
+        first, last = params[0], params[-1]
+        o0, shape = self._off[id(first)]
+        o1 = self._off[id(last)][0] + last.numel()
+        rows = sum(p.shape[0] for p in params)
+        v = buf[o0:o1].view((rows,) + tuple(shape[1:]))
+        self._cache[ck] = v
+        return v
+
+    def weight(self, params, dtype: torch.dtype) -> torch.Tensor:
+        """The compute-dtype weights of ``params`` (adjacent), as one matrix."""
+        if dtype == torch.float32:
+            return self._group(self.master, params, "master")
+        return self._group(self._shadow_buf(dtype), params, dtype)
+
+    def grad_of(self, params) -> torch.Tensor:
+        """The fp32 gradient of ``params`` (adjacent), as one matrix."""
+        return self._group(self.grad, params, "grad")
+
+    # ------------------------------------------------------------ compute copy
+    def _shadow_buf(self, dtype: torch.dtype) -> torch.Tensor:
+        buf = self._shadow.get(dtype)
+        if buf is None:
+            buf = torch.empty(self.master.numel(), dtype=dtype, device=self.device)
+            self._shadow[dtype] = buf
+            self._held = False
+        return buf
+
+    def refresh(self, dtype: torch.dtype) -> bool:
+        """Round the master weights to ``dtype`` (no-op for fp32 or inside ``hold``).
+
+        Returns True when the copy was rewritten."""
+        if dtype == torch.float32 or self._held:
+            return False
+        with torch.no_grad():
+            self._shadow_buf(dtype).copy_(self.master)
+        self.refreshes += 1
+        return True
+
+    @contextlib.contextmanager
+    def hold(self, dtype: torch.dtype):
+        """Refresh once, then keep the copy for every forward inside the block
+        (the master weights must not change inside it)."""
+        self.refresh(dtype)
+        self._held = dtype != torch.float32
+        try:
+            yield
+        finally:
+            self._held = False
+
+    # ------------------------------------------------------------ gradients
+    def attach_grads(self) -> None:
+        """Point every ``p.grad`` back at its view (after ``zero_grad(set_to_none=True)``
+        or a user assignment), keeping any gradient it held."""
+        with torch.no_grad():
+            for p, v in zip(self._params, self._gviews):
+                g = p.grad
+                if g is None:
+                    v.zero_()
+                elif g.data_ptr() != v.data_ptr():
+                    v.copy_(g)
+                else:
+                    continue
+                p.grad = v
+            if self.param.grad is None or self.param.grad.data_ptr() != self.grad.data_ptr():
+                self.param.grad = self.grad
+
+    def zero_grad(self) -> None:
+        self.grad.zero_()

@@ -1,0 +1,190 @@
+"""Projection blocks of the decoder with fused weights and fp32 weight-gradient
+accumulation (training harness; the hot-path kernels they call keep the
+reference API elsewhere).
+
+Each block takes its activations already in the compute dtype (the fused
+norms write bf16 directly), multiplies by a compute-dtype weight matrix from
+``FlatParams`` and, in backward, ADDS ``dy^T x`` in fp32 into the weight's
+slice of the flat gradient buffer (hipBLASLt with an fp32 C/D and beta 1)
+instead of returning a bf16 dW for autograd to cast and accumulate.  The
+reference (``packbalance/model/llama.py:57-103``) computes the same products
+through ``nn.Linear`` under autocast; the differences are fewer roundings:
+dW is never rounded to bf16, and the input gradient of a fused projection is
+one fp32 sum rounded once (to the input's dtype, which autograd requires)
+instead of a sum of separately rounded products.
+
+* ``qkv_rope``: q, k, v from ONE GEMM against the stacked [q; k; v] weight,
+  then RoPE on q and k (the gfx950 kernel) -- ``llama.py:89-92``.
+* ``gate_up_swiglu``: gate and up from ONE GEMM against the stacked
+  [gate; up] weight, SwiGLU (gfx950 kernel, row-strided halves) --
+  ``llama.py:57-61`` minus the down projection.
+* ``linear``: o_proj and down_proj.
+* ``embed``: the token embedding; its backward adds the gradient rows into
+  the fp32 table gradient (index_add) instead of building a dense [V, d]
+  gradient per micro-batch.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from packbalance_amd import _native as N
+from packbalance_amd.model.rope import _rope
+
+
+def _accumulate_wgrad(g: torch.Tensor, dy: torch.Tensor, x: torch.Tensor) -> None:
+    """g (fp32 [N, K]) += dy^T x, with dy [T, N] and x [T, K] in the compute dtype."""
+    if dy.dtype == torch.float32:
+        g.addmm_(dy.t(), x)
+    else:
+        torch.addmm(g, dy.t(), x, out_dtype=torch.float32, out=g)
+
+
+def _mm(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
+    if out_dtype == a.dtype:
+        return torch.mm(a, b)
+    return torch.mm(a, b, out_dtype=out_dtype)
+
+
+def _rows(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    t = t.reshape(-1, t.shape[-1])
+    if t.dtype != dtype:
+        t = t.to(dtype)
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
+class _Linear(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, w, g):
+        x2 = _rows(x, w.dtype)
+        y = torch.mm(x2, w.t())
+        ctx.save_for_backward(x2, w)
+        ctx.g, ctx.x_dtype, ctx.x_shape = g, x.dtype, x.shape
+        return y.view(*x.shape[:-1], w.shape[0])
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, w = ctx.saved_tensors
+        dy2 = _rows(dy, w.dtype)
+        dx = _mm(dy2, w, ctx.x_dtype)
+        _accumulate_wgrad(ctx.g, dy2, x2)
+        return dx.view(ctx.x_shape), None, None
+
+
+def linear(x: torch.Tensor, w: torch.Tensor, g: torch.Tensor) -> torch.Tensor:
+    """``x @ w.T``; backward returns dx in x's dtype and adds dW into ``g`` (fp32)."""
+    return _Linear.apply(x, w, g)
+
+
+class _QKVRope(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, w, g, cos, sin, hq, hkv, hd):
+        b, s, dm = x.shape
+        x2 = _rows(x, w.dtype)
+        qkv = torch.mm(x2, w.t())  # [T, (hq + 2 hkv) hd]
+        nq, nk = hq * hd, hkv * hd
+        q = qkv[:, :nq].view(b, s, hq, hd).transpose(1, 2)
+        k = qkv[:, nq:nq + nk].view(b, s, hkv, hd).transpose(1, 2)
+        v = qkv[:, nq + nk:].view(b, s, hkv, hd).transpose(1, 2)
+        qr = torch.empty((b, s, hq, hd), dtype=qkv.dtype, device=x.device).transpose(1, 2)
+        kr = torch.empty((b, s, hkv, hd), dtype=qkv.dtype, device=x.device).transpose(1, 2)
+        _rope(q, k, qr, kr, cos, sin, 0)
+        ctx.save_for_backward(x2, w, cos, sin)
+        ctx.g, ctx.dims, ctx.x_dtype = g, (b, s, dm, hq, hkv, hd), x.dtype
+        return qr, kr, v
+
+    @staticmethod
+    def backward(ctx, dq, dk, dv):
+        x2, w, cos, sin = ctx.saved_tensors
+        b, s, dm, hq, hkv, hd = ctx.dims
+        nq, nk = hq * hd, hkv * hd
+        dt = w.dtype
+        dqkv = torch.empty((b * s, nq + 2 * nk), dtype=dt, device=x2.device)
+        oq = dqkv[:, :nq].view(b, s, hq, hd).transpose(1, 2)
+        ok = dqkv[:, nq:nq + nk].view(b, s, hkv, hd).transpose(1, 2)
+        ov = dqkv[:, nq + nk:].view(b, s, hkv, hd).transpose(1, 2)
+        dq = torch.zeros_like(oq) if dq is None else dq.to(dt)
+        dk = torch.zeros_like(ok) if dk is None else dk.to(dt)
+        if dq.stride(-1) != 1:
+            dq = dq.contiguous()
+        if dk.stride(-1) != 1:
+            dk = dk.contiguous()
+        _rope(dq, dk, oq, ok, cos, sin, 1)
+        if dv is None:
+            ov.zero_()
+        else:
+            ov.copy_(dv)
+        dx = _mm(dqkv, w, ctx.x_dtype)
+        _accumulate_wgrad(ctx.g, dqkv, x2)
+        return dx.view(b, s, dm), None, None, None, None, None, None, None
+
+
+def qkv_rope(x, w, g, cos, sin, hq: int, hkv: int, hd: int):
+    """q [B, hq, S, hd] and k [B, hkv, S, hd] (RoPE applied) and v, from one GEMM
+    against the stacked [q; k; v] weight ``w``; backward adds dW into ``g``."""
+    N.require_device(x, w, op="qkv_rope")
+    if x.dim() != 3 or w.shape != ((hq + 2 * hkv) * hd, x.shape[-1]):
+        raise ValueError(f"qkv_rope: x {tuple(x.shape)} / w {tuple(w.shape)} do not match "
+                         f"hq={hq} hkv={hkv} hd={hd}")
+    return _QKVRope.apply(x, w, g, cos, sin, hq, hkv, hd)
+
+
+class _GateUpSwiGLU(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, w, g):
+        x2 = _rows(x, w.dtype)
+        gu = torch.mm(x2, w.t())  # [T, 2F]: gate | up
+        t, f2 = gu.shape
+        f = f2 // 2
+        a = torch.empty((t, f), dtype=gu.dtype, device=gu.device)
+        N.call("pb_swiglu_fwd_rows", gu.data_ptr(), f2, gu[:, f:].data_ptr(), f2, a.data_ptr(), f,
+               t, f, N.dtype_code(gu), N.stream_ptr(gu))
+        ctx.save_for_backward(x2, w, gu)
+        ctx.g, ctx.x_dtype, ctx.x_shape = g, x.dtype, x.shape
+        return a.view(*x.shape[:-1], f)
+
+    @staticmethod
+    def backward(ctx, da):
+        x2, w, gu = ctx.saved_tensors
+        t, f2 = gu.shape
+        f = f2 // 2
+        da2 = _rows(da, gu.dtype)
+        dgu = torch.empty_like(gu)
+        N.call("pb_swiglu_bwd_rows", gu.data_ptr(), f2, gu[:, f:].data_ptr(), f2, da2.data_ptr(),
+               da2.stride(0), dgu.data_ptr(), f2, dgu[:, f:].data_ptr(), f2, t, f,
+               N.dtype_code(gu), N.stream_ptr(gu))
+        dx = _mm(dgu, w, ctx.x_dtype)
+        _accumulate_wgrad(ctx.g, dgu, x2)
+        return dx.view(ctx.x_shape), None, None
+
+
+def gate_up_swiglu(x: torch.Tensor, w: torch.Tensor, g: torch.Tensor) -> torch.Tensor:
+    """``silu(x @ Wg.T) * (x @ Wu.T)`` from one GEMM against ``w`` = [Wg; Wu]."""
+    N.require_device(x, w, op="gate_up_swiglu")
+    if w.shape[0] % 2 or w.shape[1] != x.shape[-1]:
+        raise ValueError(f"gate_up_swiglu: w {tuple(w.shape)} does not match x {tuple(x.shape)}")
+    return _GateUpSwiGLU.apply(x, w, g)
+
+
+class _Embed(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, ids, weight, g):
+        ctx.save_for_backward(ids)
+        ctx.g = g
+        return F.embedding(ids, weight.detach())
+
+    @staticmethod
+    def backward(ctx, dout):
+        (ids,) = ctx.saved_tensors
+        g = ctx.g
+        g.index_add_(0, ids.reshape(-1), dout.reshape(-1, g.shape[1]).to(g.dtype))
+        return None, None, None
+
+
+def embed(ids: torch.Tensor, weight: torch.nn.Parameter, g: torch.Tensor) -> torch.Tensor:
+    """``weight[ids]``; backward adds the rows of the incoming gradient into ``g``.
+
+    ``weight`` is passed so the output joins the autograd graph; its gradient is
+    delivered through ``g`` (the returned gradient is None)."""
+    return _Embed.apply(ids, weight, g)

@@ -7,8 +7,16 @@ the block mask at :147-152 and the summed linear CE at :222-242, with the same
 dtype flow under ``torch.autocast(bf16)`` (fp32 embeddings and residual
 stream, bf16 projections, fp32 tied LM head).  Weights are random
 (``init_std`` normal, residual projections scaled by 1/sqrt(2 n_layers) as at
-:191-201).  Everything that is not a hot-path kernel (embedding, projections,
-RoPE) is plain PyTorch.
+:191-201).
+
+``forward`` is the training path: parameters live in one flat fp32 store
+(``FlatParams``) with a compute-dtype copy, q/k/v and gate/up are single
+GEMMs against stacked weights, every residual add is fused into the next
+RMSNorm (which writes the compute dtype directly: no autocast casts), and
+weight gradients accumulate in fp32 inside the backward GEMMs.  Its math is
+the reference's with fewer roundings (dW and the fused input gradients are
+never rounded to bf16).  ``forward_unfused`` is the module-by-module form
+under autocast, kept for comparison.
 """
 
 from __future__ import annotations
@@ -19,10 +27,16 @@ from dataclasses import dataclass
 import torch
 from torch import nn
 
-from packbalance_amd.kernels.fused_ce import linear_cross_entropy
-from packbalance_amd.kernels.rmsnorm import rmsnorm
+from packbalance_amd.kernels.fused_ce import (
+    linear_cross_entropy,
+    linear_cross_entropy_accumulate,
+    lmhead_weight_bf16,
+)
+from packbalance_amd.kernels.rmsnorm import add_rmsnorm, rmsnorm, rmsnorm_to
 from packbalance_amd.kernels.swiglu import swiglu
+from packbalance_amd.model import layers as L
 from packbalance_amd.model.attention import attention_forward, build_doc_block_mask
+from packbalance_amd.model.flat import FlatParams
 from packbalance_amd.model.rope import RotaryEmbedding, apply_rotary_pos_emb
 
 
@@ -85,6 +99,12 @@ class LlamaMLP(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return self.down_proj(swiglu(self.gate_proj(x), self.up_proj(x)))
 
+    def fused(self, x: torch.Tensor, flat: FlatParams, dt: torch.dtype) -> torch.Tensor:
+        gu = [self.gate_proj.weight, self.up_proj.weight]
+        a = L.gate_up_swiglu(x, flat.weight(gu, dt), flat.grad_of(gu))
+        dn = [self.down_proj.weight]
+        return L.linear(a, flat.weight(dn, dt), flat.grad_of(dn))
+
 
 class LlamaAttention(nn.Module):
     def __init__(self, cfg: ModelConfig) -> None:
@@ -105,6 +125,16 @@ class LlamaAttention(nn.Module):
         out = attention_forward(q, k, v, doc_ids, block_mask=block_mask, backend=self.backend)
         return self.o_proj(out.transpose(1, 2).contiguous().view(b, s, -1))
 
+    def fused(self, x, cos, sin, doc_ids, block_mask, flat: FlatParams, dt: torch.dtype):
+        b, s, _ = x.shape
+        qkv = [self.q_proj.weight, self.k_proj.weight, self.v_proj.weight]
+        q, k, v = L.qkv_rope(x, flat.weight(qkv, dt), flat.grad_of(qkv), cos, sin,
+                             self.n_heads, self.n_kv_heads, self.head_dim)
+        out = attention_forward(q, k, v, doc_ids, block_mask=block_mask, backend=self.backend)
+        o = out.transpose(1, 2).reshape(b, s, -1)
+        wo = [self.o_proj.weight]
+        return L.linear(o, flat.weight(wo, dt), flat.grad_of(wo))
+
 
 class LlamaDecoderLayer(nn.Module):
     def __init__(self, cfg: ModelConfig) -> None:
@@ -117,6 +147,19 @@ class LlamaDecoderLayer(nn.Module):
     def forward(self, hidden, cos, sin, doc_ids, block_mask=None):
         hidden = hidden + self.self_attn(self.input_layernorm(hidden), cos, sin, doc_ids, block_mask)
         return hidden + self.mlp(self.post_attention_layernorm(hidden))
+
+    def fused(self, hidden, pending, cos, sin, doc_ids, block_mask, flat: FlatParams,
+              dt: torch.dtype):
+        """(new residual, MLP output still to be added): the previous layer's MLP
+        output ``pending`` is added inside this layer's first norm."""
+        eps = self.input_layernorm.eps
+        if pending is None:
+            x = rmsnorm_to(hidden, self.input_layernorm.weight, eps, dt)
+        else:
+            hidden, x = add_rmsnorm(hidden, pending, self.input_layernorm.weight, eps, dt)
+        a = self.self_attn.fused(x, cos, sin, doc_ids, block_mask, flat, dt)
+        hidden, x = add_rmsnorm(hidden, a, self.post_attention_layernorm.weight, eps, dt)
+        return hidden, self.mlp.fused(x, flat, dt)
 
 
 class LlamaForCausalLM(nn.Module):
@@ -134,8 +177,56 @@ class LlamaForCausalLM(nn.Module):
         for layer in self.layers:
             nn.init.normal_(layer.self_attn.o_proj.weight, mean=0.0, std=cfg.init_std * scale)
             nn.init.normal_(layer.mlp.down_proj.weight, mean=0.0, std=cfg.init_std * scale)
+        self._flat: FlatParams | None = None
+        self._lm_bf16 = None  # (compute copy, its refresh count, wb, wt) of the tied LM head
+
+    # ------------------------------------------------------------ flat storage
+    def flat_parameters(self) -> FlatParams:
+        """The flat store of this model's parameters (created on first use, and again
+        if the parameters were moved or replaced since)."""
+        if self._flat is None or not self._flat.owns(self):
+            groups = []
+            for layer in self.layers:
+                a, m = layer.self_attn, layer.mlp
+                groups.append([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight])
+                groups.append([m.gate_proj.weight, m.up_proj.weight])
+            self._flat = FlatParams(self, groups)
+            self._lm_bf16 = None
+        return self._flat
+
+    def _lm_head(self, flat: FlatParams, dt: torch.dtype):
+        """bf16 LM-head rows and their transpose, rebuilt whenever the compute copy was."""
+        w = flat.weight([self.embed_tokens.weight], dt)
+        c = self._lm_bf16
+        if c is None or c[0] is not w or c[1] != flat.refreshes:
+            self._lm_bf16 = c = (w, flat.refreshes) + lmhead_weight_bf16(w)
+        return c[2], c[3]
 
     def forward(self, input_ids, labels, position_ids, doc_ids, block_mask=None):
+        dev = input_ids.device
+        dt = torch.get_autocast_dtype(dev.type) if torch.is_autocast_enabled(dev.type) else torch.float32
+        flat = self.flat_parameters()
+        flat.attach_grads()
+        flat.refresh(dt)
+        with torch.autocast(dev.type, enabled=False):
+            emb = [self.embed_tokens.weight]
+            hidden = L.embed(input_ids, self.embed_tokens.weight, flat.grad_of(emb))
+            cos, sin = self.rotary(position_ids)
+            if block_mask is None:
+                block_mask = build_doc_block_mask(doc_ids, self.cfg.n_heads)
+            pending = None
+            for layer in self.layers:
+                hidden, pending = layer.fused(hidden, pending, cos, sin, doc_ids, block_mask, flat, dt)
+            _, y = add_rmsnorm(hidden, pending, self.norm.weight, self.norm.eps, dt)
+            kw = dict(ignore_index=-100, z_loss_coeff=self.cfg.z_loss_coeff)
+            if dt == torch.float32 or self.cfg.d_model % 8:
+                return linear_cross_entropy(y, self.embed_tokens.weight, labels,
+                                            chunk_size=self.cfg.ce_chunk_size, **kw)
+            wb, wt = self._lm_head(flat, dt)
+            return linear_cross_entropy_accumulate(y, wb, wt, flat.grad_of(emb), labels, **kw)
+
+    def forward_unfused(self, input_ids, labels, position_ids, doc_ids, block_mask=None):
+        """Module-by-module forward (``nn.Linear`` under the caller's autocast)."""
         hidden = self.embed_tokens(input_ids)
         cos, sin = self.rotary(position_ids)
         if block_mask is None:

@@ -5,6 +5,12 @@ pack of the step (one micro-batch each) build the document block mask, run
 the forward and ``(loss / step_tokens).backward()`` under bf16 autocast; then
 ``clip_grad_norm_(1.0)`` and a fused AdamW step.
 
+The parameters live in the model's flat store (``FlatParams``): the step
+zeroes the one gradient buffer, rounds the master weights to bf16 once for
+all micro-batches (``hold``), and clips and updates the one flat parameter --
+the same AdamW arithmetic as over the per-tensor list (uniform
+hyper-parameters, element-wise update), in a single fused launch.
+
 ``capture`` records that whole sequence once into a HIP graph on static
 device buffers (every hot-path op is capture-safe: no host synchronisation,
 device-resident grad scale, all workspaces from the caching allocator);
@@ -30,7 +36,8 @@ class TrainStep:
         torch.manual_seed(seed)
         self.model = LlamaForCausalLM(cfg).to(dev)
         self.model.train()
-        self.opt = torch.optim.AdamW(self.model.parameters(), lr=lr, betas=(0.9, 0.95),
+        self.flat = self.model.flat_parameters()
+        self.opt = torch.optim.AdamW([self.flat.param], lr=lr, betas=(0.9, 0.95),
                                      weight_decay=0.1, fused=True, capturable=True)
 
         def z():
@@ -45,14 +52,16 @@ class TrainStep:
 
     def _body(self, batches, step_tokens) -> None:
         self.loss_sum.zero_()
-        with torch.autocast("cuda", dtype=torch.bfloat16):
+        self.flat.attach_grads()
+        self.flat.zero_grad()
+        with torch.autocast("cuda", dtype=torch.bfloat16), self.flat.hold(torch.bfloat16):
             for b in batches:
                 bm = build_doc_block_mask(b["doc_ids"], self.cfg.n_heads)
                 loss = self.model(b["input_ids"], b["labels"], b["position_ids"], b["doc_ids"],
                                   block_mask=bm)
                 (loss / step_tokens).backward()
                 self.loss_sum += loss.detach()
-        norm = torch.nn.utils.clip_grad_norm_(self.model.parameters(), 1.0)
+        norm = torch.nn.utils.clip_grad_norm_([self.flat.param], 1.0)
         self.grad_norm.copy_(norm)
         self.opt.step()
 
@@ -62,7 +71,6 @@ class TrainStep:
                      doc_ids=b.doc_ids) for b in batch_list]
 
     def eager(self, batch_list) -> None:
-        self.opt.zero_grad(set_to_none=True)
         tokens = float(sum(b.useful_tokens for b in batch_list))
         self._body(self._as_dicts(batch_list), tokens)
 
@@ -81,10 +89,8 @@ class TrainStep:
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
             for _ in range(warmup_steps):
-                self.opt.zero_grad(set_to_none=True)
                 self._body(self.static, self.step_tokens)
         torch.cuda.current_stream().wait_stream(side)
-        self.opt.zero_grad(set_to_none=True)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
             self._body(self.static, self.step_tokens)

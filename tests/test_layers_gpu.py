@@ -1,0 +1,149 @@
+"""GPU checks of the decoder's fused projection blocks (training harness).
+
+Each block is compared with the same computation in torch fp32 on the same
+bf16 operands: outputs within bf16 rounding (2e-2 relative Frobenius norm
+for products that are rounded to bf16 once or twice), input gradients (in
+the input's dtype) and fp32 weight gradients within 1e-2 relative Frobenius
+norm.  Weight gradients
+are ADDED to a non-zero accumulator, and the test subtracts the starting
+value, so accumulation (not overwrite) is what is checked; a second backward
+must add the same amount again.
+The LM-head CE that accumulates dW is compared with ``linear_cross_entropy``
+(the same kernels): identical loss and dx, dW equal to the accumulator's
+increase within fp32 rounding.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from packbalance_amd.kernels.fused_ce import (
+    linear_cross_entropy,
+    linear_cross_entropy_accumulate,
+    lmhead_weight_bf16,
+)
+from packbalance_amd.model import layers as L
+from packbalance_amd.model.rope import RotaryEmbedding
+
+pytestmark = pytest.mark.gpu
+
+BF = torch.bfloat16
+
+
+def _rel(got: torch.Tensor, want: torch.Tensor) -> float:
+    g, w = got.detach().double(), want.detach().double()
+    return float((g - w).norm() / w.norm().clamp_min(1e-30))
+
+
+def _rope_ref(x, cos, sin):
+    h = x.shape[-1] // 2
+    c, s = cos[:, None], sin[:, None]  # [B, 1, S, D/2]
+    x1, x2 = x[..., :h], x[..., h:]
+    return torch.cat((x1 * c - x2 * s, x2 * c + x1 * s), dim=-1)
+
+
+@pytest.mark.parametrize("b,s,dm,hq,hkv,hd", [(1, 2048, 768, 12, 4, 64), (2, 256, 128, 4, 2, 32)])
+def test_qkv_rope_matches_fp32(b, s, dm, hq, hkv, hd, dev) -> None:
+    g = torch.Generator().manual_seed(0)
+    n = (hq + 2 * hkv) * hd
+    x = torch.randn(b, s, dm, generator=g).to(dev, BF)
+    w = (torch.randn(n, dm, generator=g) * 0.05).to(dev, BF)
+    acc0 = torch.randn(n, dm, generator=g).to(dev)
+    acc = acc0.clone()
+    pos = torch.randint(0, s, (b, s), generator=g).to(dev)
+    cos, sin = RotaryEmbedding(hd, s).to(dev)(pos)
+    xr = x.clone().requires_grad_(True)
+    q, k, v = L.qkv_rope(xr, w, acc, cos, sin, hq, hkv, hd)
+    assert q.shape == (b, hq, s, hd) and k.shape == (b, hkv, s, hd) and v.shape == (b, hkv, s, hd)
+    gq, gk, gv = (torch.randn(t.shape, generator=g).to(dev, BF) for t in (q, k, v))
+    torch.autograd.backward((q, k, v), (gq, gk, gv))
+
+    xf = x.float().requires_grad_(True)
+    wf = w.float().requires_grad_(True)
+    qkv = xf @ wf.t()
+    nq, nk = hq * hd, hkv * hd
+    qf = _rope_ref(qkv[..., :nq].view(b, s, hq, hd).transpose(1, 2), cos, sin)
+    kf = _rope_ref(qkv[..., nq:nq + nk].view(b, s, hkv, hd).transpose(1, 2), cos, sin)
+    vf = qkv[..., nq + nk:].view(b, s, hkv, hd).transpose(1, 2)
+    torch.autograd.backward((qf, kf, vf), (gq.float(), gk.float(), gv.float()))
+    for got, want, name in ((q, qf, "q"), (k, kf, "k"), (v, vf, "v")):
+        assert _rel(got, want) < 2e-2, name
+    assert xr.grad.dtype == BF
+    assert _rel(xr.grad, xf.grad) < 1e-2
+    assert _rel(acc - acc0, wf.grad) < 1e-2
+    # A second backward over a fresh forward adds the same amount again.
+    q, k, v = L.qkv_rope(x.clone().requires_grad_(True), w, acc, cos, sin, hq, hkv, hd)
+    torch.autograd.backward((q, k, v), (gq, gk, gv))
+    assert _rel(acc - acc0, 2 * wf.grad) < 1e-2
+
+
+@pytest.mark.parametrize("t,dm,f", [(2048, 768, 2048), (256, 128, 344)])
+def test_gate_up_swiglu_and_down_proj_match_fp32(t, dm, f, dev) -> None:
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(1, t, dm, generator=g).to(dev, BF)
+    wgu = (torch.randn(2 * f, dm, generator=g) * 0.05).to(dev, BF)
+    wd = (torch.randn(dm, f, generator=g) * 0.05).to(dev, BF)
+    agu0 = torch.randn(2 * f, dm, generator=g).to(dev)
+    ad0 = torch.randn(dm, f, generator=g).to(dev)
+    agu, ad = agu0.clone(), ad0.clone()
+    xr = x.clone().requires_grad_(True)
+    a = L.gate_up_swiglu(xr, wgu, agu)
+    y = L.linear(a, wd, ad)
+    assert a.dtype == BF and y.dtype == BF and y.shape == (1, t, dm)
+    gy = torch.randn(y.shape, generator=g).to(dev, BF)
+    y.backward(gy)
+
+    xf = x.float().requires_grad_(True)
+    wguf = wgu.float().requires_grad_(True)
+    wdf = wd.float().requires_grad_(True)
+    gu = xf @ wguf.t()
+    af = torch.nn.functional.silu(gu[..., :f]) * gu[..., f:]
+    yf = af @ wdf.t()
+    yf.backward(gy.float())
+    assert _rel(a, af) < 2e-2
+    assert _rel(y, yf) < 2e-2
+    assert xr.grad.dtype == BF and _rel(xr.grad, xf.grad) < 1e-2
+    assert _rel(agu - agu0, wguf.grad) < 1e-2
+    assert _rel(ad - ad0, wdf.grad) < 1e-2
+
+
+def test_embed_accumulates_rows(dev) -> None:
+    g = torch.Generator().manual_seed(2)
+    v, d = 512, 64
+    w = torch.nn.Parameter(torch.randn(v, d, generator=g).to(dev))
+    acc0 = torch.randn(v, d, generator=g).to(dev)
+    acc = acc0.clone()
+    ids = torch.randint(0, 40, (2, 300), generator=g).to(dev)  # many repeats
+    out = L.embed(ids, w, acc)
+    assert torch.equal(out, w.detach()[ids])
+    go = torch.randn(out.shape, generator=g).to(dev)
+    out.backward(go)
+    assert w.grad is None  # delivered through the accumulator
+    want = torch.zeros(v, d, device=dev).index_add_(0, ids.reshape(-1), go.reshape(-1, d))
+    torch.testing.assert_close(acc - acc0, want, rtol=1e-5, atol=1e-5)
+
+
+def test_lmhead_ce_accumulate_matches_linear_ce(dev) -> None:
+    g = torch.Generator().manual_seed(3)
+    n, v, d = 2048, 32000, 768
+    x = torch.randn(1, n, d, generator=g).to(dev, BF)
+    w = (torch.randn(v, d, generator=g) * 0.02).to(dev)
+    t = torch.randint(0, v, (1, n), generator=g)
+    t[0, ::37] = -100
+    t = t.to(dev)
+    xr = x.clone().requires_grad_(True)
+    wr = w.clone().requires_grad_(True)
+    loss = linear_cross_entropy(xr, wr, t)
+    loss.backward()
+    wb, wt = lmhead_weight_bf16(w)  # the packing linear_cross_entropy applies to W
+    acc0 = torch.randn(v, d, generator=g).to(dev)
+    acc = acc0.clone()
+    xa = x.clone().requires_grad_(True)
+    loss_a = linear_cross_entropy_accumulate(xa, wb, wt, acc, t)
+    (loss_a * 1.0).backward()
+    assert torch.equal(loss_a, loss)
+    assert torch.equal(xa.grad, xr.grad)
+    torch.testing.assert_close(acc - acc0, wr.grad, rtol=1e-5, atol=1e-5)
+    with pytest.raises(ValueError):
+        linear_cross_entropy_accumulate(xa, wb, wt, acc.to(BF), t)

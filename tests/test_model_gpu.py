@@ -48,6 +48,48 @@ def test_cfg1_forward_backward_matches_eager_cpu_path(dev) -> None:
         assert rel < 2e-2, f"{name}: relative grad error {rel:.3e}"
 
 
+def test_cfg1_bf16_fused_path_no_less_accurate_than_module_path(dev) -> None:
+    """Under bf16 autocast, the training path (fused QKV / gate-up GEMMs, residual adds
+    inside the norms, fp32 weight-gradient accumulation) against the fp64 oracle must be
+    no worse than the module-by-module autocast path -- the reference's own dtype flow
+    (llama.py under torch.autocast) -- on the same weights: per parameter, relative
+    gradient error <= 1.5x the module path's + 1e-3, and the same for the summed loss."""
+    cfg = cfg1_model()
+    torch.manual_seed(0)
+    model = LlamaForCausalLM(cfg).to(dev)
+    packs = W.cfg1_packs(seed=0)
+    batch = W.pack_tensors(packs, 256, cfg.vocab_size, np.random.default_rng(0))
+    params = OM.cpu_params(model, torch.float64)
+    args = [(batch.input_ids[i:i + 1], batch.labels[i:i + 1], batch.position_ids[i:i + 1],
+             batch.doc_ids[i:i + 1]) for i in range(len(packs))]
+    ref_total = 0.0
+    for a in args:
+        ref = OM.loss(params, cfg, *a)
+        ref.backward()
+        ref_total += float(ref)
+
+    def run(fn):
+        model.zero_grad(set_to_none=True)
+        total = 0.0
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            for a in args:
+                loss = fn(*(t.to(dev) for t in a))
+                loss.backward()
+                total += float(loss)
+        return total, {n: p.grad.double().cpu().clone() for n, p in model.named_parameters()}
+
+    lu, gu = run(model.forward_unfused)
+    lf, gf = run(model.forward)
+    eu, ef = abs(lu - ref_total) / abs(ref_total), abs(lf - ref_total) / abs(ref_total)
+    print(f"loss rel err: module path {eu:.2e}, fused path {ef:.2e}")
+    assert ef <= 1.5 * eu + 1e-3, (ef, eu)
+    for name, r in ((n, p.grad) for n, p in params.items()):
+        rn = r.norm().clamp_min(1e-30)
+        e_u = float((gu[name] - r).norm() / rn)
+        e_f = float((gf[name] - r).norm() / rn)
+        assert e_f <= 1.5 * e_u + 1e-3, f"{name}: fused {e_f:.3e} vs module path {e_u:.3e}"
+
+
 def test_cfg2_model_step_runs_under_autocast(dev) -> None:
     """cfg2 shape (100M params): one bf16-autocast micro-batch gives a finite loss near ln(V)."""
     cfg = cfg2_model()

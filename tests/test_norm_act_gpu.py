@@ -12,6 +12,7 @@ import pytest
 import torch
 
 from oracle import kernels as OK
+from packbalance_amd import _native as N
 from packbalance_amd.kernels.rmsnorm import rmsnorm
 from packbalance_amd.kernels.swiglu import swiglu
 
@@ -162,6 +163,44 @@ def test_swiglu_cfg5_full_size(dev) -> None:
         torch.testing.assert_close(gr.grad[r : r + 4096].float(), d * u * s * (1 + g * (1 - s)),
                                    rtol=1e-2, atol=1e-2)
         torch.testing.assert_close(ur.grad[r : r + 4096].float(), d * g * s, rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize(
+    "rows,cols,dtype",
+    [
+        (2048, 2048, torch.bfloat16),  # cfg2 fused gate|up projection
+        (256, 344, torch.bfloat16),  # cfg1 ffn
+        (37, 333, torch.bfloat16),  # cols % 8 != 0: scalar path
+        (64, 96, torch.float32),
+    ],
+)
+def test_swiglu_rows_on_fused_halves_match_oracle(rows, cols, dtype, dev) -> None:
+    """gate/up are the halves of one [rows, 2*cols] buffer and dgate/dup are written
+    back into one such buffer (pb_swiglu_fwd_rows / pb_swiglu_bwd_rows)."""
+    g0 = torch.Generator().manual_seed(1)
+    gu = torch.randn(rows, 2 * cols, generator=g0).to(dev, dtype)
+    dy = torch.randn(rows, cols, generator=g0).to(dev, dtype)
+    gate, up = gu[:, :cols], gu[:, cols:]
+    out = torch.full((rows, cols), float("nan"), dtype=dtype, device=dev)
+    st, code = N.stream_ptr(gu), N.dtype_code(gu)
+    N.call("pb_swiglu_fwd_rows", gate.data_ptr(), 2 * cols, up.data_ptr(), 2 * cols,
+           out.data_ptr(), cols, rows, cols, code, st)
+    dgu = torch.full_like(gu, float("nan"))
+    N.call("pb_swiglu_bwd_rows", gate.data_ptr(), 2 * cols, up.data_ptr(), 2 * cols,
+           dy.data_ptr(), cols, dgu.data_ptr(), 2 * cols, dgu[:, cols:].data_ptr(), 2 * cols,
+           rows, cols, code, st)
+    tol = TOL[dtype]
+    _close(out, OK.swiglu_fwd(gate, up), tol, "out")
+    dg, du = OK.swiglu_bwd(gate, up, dy)
+    _close(dgu[:, :cols], dg, tol, "dgate")
+    _close(dgu[:, cols:], du, tol, "dup")
+
+
+def test_swiglu_rows_rejects_bad_strides(dev) -> None:
+    x = torch.zeros(4, 8, device=dev, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        N.call("pb_swiglu_fwd_rows", x.data_ptr(), 4, x.data_ptr(), 8, x.data_ptr(), 8, 4, 8,
+               N.dtype_code(x), N.stream_ptr(x))
 
 
 def test_swiglu_rejects_cpu() -> None:
