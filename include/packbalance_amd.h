@@ -233,7 +233,8 @@ int pb_lmhead_ce_bwd(const void *x, int64_t ldx, const void *w, int64_t ldw, con
  * Backward (workspace: pb_add_rmsnorm_bwd_workspace_bytes):
  *   d = rstd*(dy*w - h_hat*mean(dy*w*h_hat)) + dres  (dres may be NULL)
  *   dx = d in h_dtype, ddelta = d in ddelta_dtype (may be NULL),
- *   dw = sum_rows dy*h_hat in w_dtype.   dx may alias dres.
+ *   dw = sum_rows dy*h_hat in w_dtype (dw_accumulate != 0: fp32 w and dw,
+ *   and the sum is added to dw).   dx may alias dres.
  * Unit inner stride; row strides in elements.                                */
 int pb_add_rmsnorm_fwd(const void *x, int64_t x_row_stride, int x_dtype, const void *delta,
                        int64_t delta_row_stride, int delta_dtype, void *h_out,
@@ -245,8 +246,30 @@ int pb_add_rmsnorm_bwd(const void *dy, int64_t dy_row_stride, int dy_dtype, cons
                        int64_t h_row_stride, int h_dtype, const void *w, int w_dtype,
                        const float *rstd, const void *dres, int64_t dres_row_stride, void *dx,
                        int64_t dx_row_stride, void *ddelta, int64_t ddelta_row_stride,
-                       int ddelta_dtype, void *dw, void *workspace, int64_t rows, int64_t n,
-                       void *stream);
+                       int ddelta_dtype, void *dw, int dw_accumulate, void *workspace,
+                       int64_t rows, int64_t n, void *stream);
+
+/* ---- Clip-by-global-norm + AdamW over one flat fp32 buffer --------------
+ * Replaces torch.nn.utils.clip_grad_norm_(params, max_grad_norm) followed by
+ * torch.optim.AdamW(params, lr, (beta1, beta2), eps, weight_decay,
+ * fused=True).step() as the reference's train loop calls them
+ * (packbalance/train/train.py:58-69,353-362; profiling/bench_train.py:79-85,
+ * 115-116), for uniform hyper-parameters over parameters stored as one flat
+ * buffer:
+ *   norm = ||grad||_2 -> *grad_norm_out (may be NULL);
+ *   c = min(max_grad_norm / (norm + 1e-6), 1)  (1 when max_grad_norm <= 0);
+ *   *step += 1 (device fp32, the optimizer's step count);
+ *   p -= lr*wd*p;  m = b1 m + (1-b1) c g;  v = b2 v + (1-b2) (c g)^2;
+ *   p -= lr/(1-b1^t) * m / (sqrt(v)/sqrt(1-b2^t) + eps);
+ *   param_copy (may be NULL) = p rounded to copy_dtype.
+ * grad is read, never written (the clipped gradient is not stored back).
+ * Buffers 16-byte aligned (param_copy 8-byte); workspace:
+ * pb_clip_adamw_workspace_bytes(n) bytes, 16-byte aligned.                  */
+int64_t pb_clip_adamw_workspace_bytes(int64_t n);
+int pb_clip_adamw_step(float *param, const float *grad, float *exp_avg, float *exp_avg_sq,
+                       void *param_copy, int copy_dtype, int64_t n, float lr, float beta1,
+                       float beta2, float eps, float weight_decay, float max_grad_norm,
+                       float *step, float *grad_norm_out, void *workspace, void *stream);
 
 /* ---- Rotary position embedding (q and k in one launch) ------------------
  * Replaces packbalance/model/rope.py:34-42 (apply_rotary_pos_emb, NeoX

@@ -12,6 +12,8 @@ Modules (each function cites the reference file:line it follows):
               (packbalance/model/attention.py)
   block_mask  FlexAttention BlockMask tables from doc_ids
               (torch.nn.attention.flex_attention.create_block_mask semantics)
+  optim       gradient clipping + AdamW step (torch.nn.utils.clip_grad_norm_ +
+              torch.optim.AdamW, as the reference's train loop calls them)
 
 How each function is pinned (beyond restating its formula) is listed in
 ``tests/test_oracle.py``; every oracle function has at least one check there

@@ -100,8 +100,13 @@ SIGNATURES: dict[str, tuple] = {
     "pb_add_rmsnorm_bwd_workspace_bytes": (_i64, [_i64, _i64]),
     "pb_add_rmsnorm_bwd": (
         _i32,
-        [_p, _i64, _i32, _p, _i64, _i32, _p, _i32, _p, _p, _i64, _p, _i64, _p, _i64, _i32, _p, _p,
-         _i64, _i64, _p],
+        [_p, _i64, _i32, _p, _i64, _i32, _p, _i32, _p, _p, _i64, _p, _i64, _p, _i64, _i32, _p, _i32,
+         _p, _i64, _i64, _p],
+    ),
+    "pb_clip_adamw_workspace_bytes": (_i64, [_i64]),
+    "pb_clip_adamw_step": (
+        _i32,
+        [_p, _p, _p, _p, _p, _i32, _i64, _f32, _f32, _f32, _f32, _f32, _f32, _p, _p, _p, _p],
     ),
     "pb_rope_qk": (
         _i32,

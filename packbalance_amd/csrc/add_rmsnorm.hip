@@ -304,30 +304,43 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_bwd_loop(AddNormBwd a) {
   }
 }
 
-// dw[c] = sum_p partial[p, c] in dtype wdt.
-__global__ __launch_bounds__(1024) void add_rmsnorm_dw_reduce(const float *__restrict__ partial,
-                                                              char *dw, int wdt, int nparts,
-                                                              int n) {
-  __shared__ float red[16][64];
-  const int lane = threadIdx.x & 63, grp = threadIdx.x >> 6;
-  const int col = blockIdx.x * 64 + lane;
+// dw[c] = sum_p partial[p, c] in dtype wdt, or dw[c] += that sum (fp32 dw)
+// when accumulate is set.  A workgroup owns 16 columns; its 16 part-lanes
+// sum every 16th partial row (fixed order, so the result is deterministic)
+// and are folded in LDS.  Small column tiles keep n / 16 workgroups busy
+// on the few-hundred-row partial tables the backward leaves.
+constexpr int kRedCols = 16, kRedParts = 16;
+__global__ __launch_bounds__(kRedCols *kRedParts) void add_rmsnorm_dw_reduce(
+    const float *__restrict__ partial, char *dw, int wdt, int nparts, int n, int accumulate) {
+  __shared__ float red[kRedParts][kRedCols];
+  const int cl = threadIdx.x % kRedCols, pl = threadIdx.x / kRedCols;
+  const int col = blockIdx.x * kRedCols + cl;
   float s0 = 0.f, s1 = 0.f;
   if (col < n) {
-    int p = grp;
-    for (; p + 16 < nparts; p += 32) {
+    int p = pl;
+    for (; p + kRedParts < nparts; p += 2 * kRedParts) {
       s0 += partial[(int64_t)p * n + col];
-      s1 += partial[(int64_t)(p + 16) * n + col];
+      s1 += partial[(int64_t)(p + kRedParts) * n + col];
     }
-    for (; p < nparts; p += 16) s0 += partial[(int64_t)p * n + col];
+    if (p < nparts) s0 += partial[(int64_t)p * n + col];
   }
-  red[grp][lane] = s0 + s1;
+  red[pl][cl] = s0 + s1;
   __syncthreads();
-  if (grp == 0 && col < n) {
+  if (pl == 0 && col < n) {
     float t = 0.f;
 #pragma unroll
-    for (int g = 0; g < 16; ++g) t += red[g][lane];
-    st1(dw + (int64_t)col * esize(wdt), wdt, t);
+    for (int g = 0; g < kRedParts; ++g) t += red[g][cl];
+    if (accumulate)
+      reinterpret_cast<float *>(dw)[col] += t;
+    else
+      st1(dw + (int64_t)col * esize(wdt), wdt, t);
   }
+}
+
+// dw = 0 (or unchanged when accumulating) for an empty batch.
+__global__ __launch_bounds__(256) void add_rmsnorm_dw_zero(char *dw, int wdt, int n) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c < n) st1(dw + (int64_t)c * esize(wdt), wdt, 0.f);
 }
 
 int bwd_nwg(int64_t rows, int &rows_per_wg) {
@@ -364,11 +377,11 @@ extern "C" int pb_add_rmsnorm_fwd(const void *x, int64_t x_row_stride, int x_dty
   PB_CHECK_ARG(rows >= 0 && n > 0, "pb_add_rmsnorm_fwd: bad shape rows=%lld n=%lld",
                (long long)rows, (long long)n);
   PB_CHECK_SUPPORTED(n <= 65536, "RMSNorm feature dimension is too large for this kernel");
-  PB_CHECK_ARG(x && w && y && rstd, "pb_add_rmsnorm_fwd: null argument");
   PB_CHECK_ARG(x_row_stride >= n && y_row_stride >= n && (!delta || delta_row_stride >= n) &&
                    (!h_out || h_row_stride >= n),
                "pb_add_rmsnorm_fwd: row stride < n");
-  if (rows == 0) return PB_OK;
+  if (rows == 0) return PB_OK;  // empty tensors may carry null pointers
+  PB_CHECK_ARG(x && w && y && rstd, "pb_add_rmsnorm_fwd: null argument");
   AddNormFwd a;
   a.x = static_cast<const char *>(x);
   a.delta = static_cast<const char *>(delta);
@@ -409,8 +422,8 @@ extern "C" int pb_add_rmsnorm_bwd(const void *dy, int64_t dy_row_stride, int dy_
                                   int w_dtype, const float *rstd, const void *dres,
                                   int64_t dres_row_stride, void *dx, int64_t dx_row_stride,
                                   void *ddelta, int64_t ddelta_row_stride, int ddelta_dtype,
-                                  void *dw, void *workspace, int64_t rows, int64_t n,
-                                  void *stream) {
+                                  void *dw, int dw_accumulate, void *workspace, int64_t rows,
+                                  int64_t n, void *stream) {
   using namespace pb;
   clear_error();
   PB_CHECK_ARG(valid_dtype(dy_dtype) && valid_dtype(h_dtype) && valid_dtype(w_dtype) &&
@@ -418,15 +431,20 @@ extern "C" int pb_add_rmsnorm_bwd(const void *dy, int64_t dy_row_stride, int dy_
                "pb_add_rmsnorm_bwd: bad dtype");
   PB_CHECK_ARG(rows >= 0 && n > 0, "pb_add_rmsnorm_bwd: bad shape");
   PB_CHECK_SUPPORTED(n <= 65536, "RMSNorm feature dimension is too large for this kernel");
-  PB_CHECK_ARG(dy && h && w && rstd && dx && dw, "pb_add_rmsnorm_bwd: null argument");
+  PB_CHECK_ARG(w && dw, "pb_add_rmsnorm_bwd: null weight or dw");
+  PB_CHECK_ARG(!dw_accumulate || w_dtype == PB_F32,
+               "pb_add_rmsnorm_bwd: dw_accumulate needs an fp32 weight (and dw)");
   PB_CHECK_ARG(dy_row_stride >= n && h_row_stride >= n && dx_row_stride >= n &&
                    (!dres || dres_row_stride >= n) && (!ddelta || ddelta_row_stride >= n),
                "pb_add_rmsnorm_bwd: row stride < n");
   hipStream_t st = as_stream(stream);
   if (rows == 0) {
-    (void)hipMemsetAsync(dw, 0, (size_t)n * dtype_bytes(w_dtype), st);
+    if (!dw_accumulate)
+      hipLaunchKernelGGL(add_rmsnorm_dw_zero, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                         static_cast<char *>(dw), w_dtype, (int)n);
     return launch_status("pb_add_rmsnorm_bwd(empty)");
   }
+  PB_CHECK_ARG(dy && h && rstd && dx, "pb_add_rmsnorm_bwd: null argument");
   PB_CHECK_ARG(workspace != nullptr, "pb_add_rmsnorm_bwd: workspace is required");
   AddNormBwd a;
   a.dy = static_cast<const char *>(dy);
@@ -459,7 +477,8 @@ extern "C" int pb_add_rmsnorm_bwd(const void *dy, int64_t dy_row_stride, int dy_
   }
   int s = launch_status("pb_add_rmsnorm_bwd");
   if (s) return s;
-  hipLaunchKernelGGL(add_rmsnorm_dw_reduce, dim3((unsigned)((n + 63) / 64)), dim3(1024), 0, st,
-                     a.partial, static_cast<char *>(dw), w_dtype, nwg, (int)n);
+  hipLaunchKernelGGL(add_rmsnorm_dw_reduce, dim3((unsigned)((n + kRedCols - 1) / kRedCols)),
+                     dim3(kRedCols * kRedParts), 0, st, a.partial, static_cast<char *>(dw), w_dtype,
+                     nwg, (int)n, dw_accumulate ? 1 : 0);
   return launch_status("pb_add_rmsnorm_bwd(dw)");
 }

@@ -454,7 +454,9 @@ extern "C" int pb_lmhead_ce_fwd(const void *x, int64_t ldx, const void *w, int64
                "pb_lmhead_ce_fwd: x/w rows must be 16-byte aligned with d %% 8 == 0");
   hipStream_t st = as_stream(stream);
   if (n == 0) {
-    (void)hipMemsetAsync(loss_sum, 0, sizeof(float), st);
+    // The fixed-order sum over no rows writes 0 (a kernel, so graph capture
+    // records no memset node).
+    hipLaunchKernelGGL(sum_rows, dim3(1), dim3(1024), 0, st, (const float *)nullptr, 0, loss_sum);
     return launch_status("pb_lmhead_ce_fwd(empty)");
   }
   const int nmt = (int)((v + BM - 1) / BM);

@@ -422,6 +422,17 @@ int bwd_w(int wdt, const void *dy, int64_t dys, const void *x, int64_t xs, const
   }
 }
 
+// dw = 0 for an empty batch (a kernel, not a memset, so graph capture records no
+// memset node).
+__global__ __launch_bounds__(256) void rmsnorm_dw_zero(char *dw, int bytes_per, int64_t n) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= n) return;
+  if (bytes_per == 4)
+    reinterpret_cast<float *>(dw)[c] = 0.f;
+  else
+    reinterpret_cast<uint16_t *>(dw)[c] = 0;
+}
+
 }  // namespace
 }  // namespace pb
 
@@ -463,7 +474,9 @@ extern "C" int pb_rmsnorm_bwd(const void *dy, int64_t dy_row_stride, const void 
   hipStream_t st = as_stream(stream);
   if (rows == 0) {
     // dw of an empty batch is zero.
-    (void)hipMemsetAsync(dw, 0, (size_t)n * dtype_bytes(w_dtype), st);
+    PB_CHECK_ARG(dw != nullptr, "pb_rmsnorm_bwd: null dw");
+    hipLaunchKernelGGL(rmsnorm_dw_zero, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                       static_cast<char *>(dw), dtype_bytes(w_dtype), n);
     return launch_status("pb_rmsnorm_bwd(empty)");
   }
   PB_CHECK_ARG(workspace != nullptr, "pb_rmsnorm_bwd: workspace is required");

@@ -99,7 +99,7 @@ def _fwd_call(x2d, d2d, h, w, y, rstd, eps):
     )
 
 
-def _bwd_call(dy2d, h2d, w, rstd, dres, dx, ddelta, dw):
+def _bwd_call(dy2d, h2d, w, rstd, dres, dx, ddelta, dw, accumulate=False):
     rows, n = h2d.shape
     ws_bytes = N.lib().pb_add_rmsnorm_bwd_workspace_bytes(rows, n)
     ws = torch.empty(max(1, ws_bytes // 4), dtype=torch.float32, device=h2d.device)
@@ -113,8 +113,16 @@ def _bwd_call(dy2d, h2d, w, rstd, dres, dx, ddelta, dw):
         ddelta.data_ptr() if ddelta is not None else None,
         ddelta.stride(0) if ddelta is not None else n,
         N.dtype_code(ddelta) if ddelta is not None else N.dtype_code(dx),
-        dw.data_ptr(), ws.data_ptr(), rows, n, N.stream_ptr(h2d),
+        dw.data_ptr(), int(accumulate), ws.data_ptr(), rows, n, N.stream_ptr(h2d),
     )
+
+
+def _check_acc(dw_acc, weight):
+    if dw_acc is None:
+        return
+    if (dw_acc.dtype != torch.float32 or weight.dtype != torch.float32
+            or dw_acc.shape != weight.shape or not dw_acc.is_contiguous()):
+        raise ValueError("dw_acc must be a contiguous fp32 tensor shaped like an fp32 weight")
 
 
 def _check(x, weight, op):
@@ -128,8 +136,9 @@ def _check(x, weight, op):
 
 class _AddRMSNorm(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, delta, weight, eps, out_dtype):
+    def forward(ctx, x, delta, weight, eps, out_dtype, dw_acc):
         _check(x, weight, "add_rmsnorm")
+        _check_acc(dw_acc, weight)
         if delta.shape != x.shape:
             raise ValueError(f"add_rmsnorm: delta {tuple(delta.shape)} and x {tuple(x.shape)} differ")
         x2d, d2d, w = _rows(x), _rows(delta), weight.contiguous()
@@ -140,6 +149,7 @@ class _AddRMSNorm(torch.autograd.Function):
         _fwd_call(x2d, d2d, h, w, y, rstd, eps)
         ctx.save_for_backward(h, w, rstd)
         ctx.meta = (x.shape, delta.dtype, weight.dtype)
+        ctx.dw_acc = dw_acc
         return h.reshape(x.shape), y.reshape(x.shape)
 
     @staticmethod
@@ -154,17 +164,21 @@ class _AddRMSNorm(torch.autograd.Function):
             dres = dres if dres.dtype == h.dtype else dres.to(h.dtype)
         dx = torch.empty_like(h)
         ddelta = torch.empty((rows, n), dtype=delta_dtype, device=h.device)
+        if ctx.dw_acc is not None:
+            _bwd_call(dy2d, h, w, rstd, dres, dx, ddelta, ctx.dw_acc, accumulate=True)
+            return dx.reshape(shape), ddelta.reshape(shape), None, None, None, None
         dw = torch.empty(n, dtype=w.dtype, device=w.device)
         _bwd_call(dy2d, h, w, rstd, dres, dx, ddelta, dw)
-        return dx.reshape(shape), ddelta.reshape(shape), dw.to(w_dtype), None, None
+        return dx.reshape(shape), ddelta.reshape(shape), dw.to(w_dtype), None, None, None
 
 
 class _RMSNormTo(torch.autograd.Function):
     """RMSNorm whose output dtype differs from the input's (no residual add)."""
 
     @staticmethod
-    def forward(ctx, x, weight, eps, out_dtype):
+    def forward(ctx, x, weight, eps, out_dtype, dw_acc):
         _check(x, weight, "rmsnorm")
+        _check_acc(dw_acc, weight)
         x2d, w = _rows(x), weight.contiguous()
         rows, n = x2d.shape
         y = torch.empty((rows, n), dtype=out_dtype, device=x.device)
@@ -172,6 +186,7 @@ class _RMSNormTo(torch.autograd.Function):
         _fwd_call(x2d, None, None, w, y, rstd, eps)
         ctx.save_for_backward(x2d, w, rstd)
         ctx.meta = (x.shape, weight.dtype)
+        ctx.dw_acc = dw_acc
         return y.reshape(x.shape)
 
     @staticmethod
@@ -179,26 +194,32 @@ class _RMSNormTo(torch.autograd.Function):
         x2d, w, rstd = ctx.saved_tensors
         shape, w_dtype = ctx.meta
         dx = torch.empty_like(x2d)
+        if ctx.dw_acc is not None:
+            _bwd_call(_rows(dy), x2d, w, rstd, None, dx, None, ctx.dw_acc, accumulate=True)
+            return dx.reshape(shape), None, None, None, None
         dw = torch.empty(x2d.shape[1], dtype=w.dtype, device=w.device)
         _bwd_call(_rows(dy), x2d, w, rstd, None, dx, None, dw)
-        return dx.reshape(shape), dw.to(w_dtype), None, None
+        return dx.reshape(shape), dw.to(w_dtype), None, None, None
 
 
 def add_rmsnorm(x: torch.Tensor, delta: torch.Tensor, weight: torch.Tensor, eps: float,
-                out_dtype: torch.dtype | None = None):
+                out_dtype: torch.dtype | None = None, dw_acc: torch.Tensor | None = None):
     """Residual add fused with the next RMSNorm (gfx950 kernel).
 
     Returns ``(h, y)``: ``h = x + delta`` in x's dtype (the new residual stream) and
     ``y = rmsnorm(h, weight, eps)`` in ``out_dtype`` (default x's dtype).  The backward
     takes the gradients of both outputs and returns them summed into ``dx`` (x's dtype)
-    and ``ddelta`` (delta's dtype), so no separate add or cast kernels run.
+    and ``ddelta`` (delta's dtype), so no separate add or cast kernels run.  With
+    ``dw_acc`` (fp32, shaped like an fp32 ``weight``) the weight gradient is ADDED to
+    ``dw_acc`` by the backward kernel and the gradient returned for ``weight`` is None.
     """
-    return _AddRMSNorm.apply(x, delta, weight, eps, out_dtype or x.dtype)
+    return _AddRMSNorm.apply(x, delta, weight, eps, out_dtype or x.dtype, dw_acc)
 
 
 def rmsnorm_to(x: torch.Tensor, weight: torch.Tensor, eps: float,
-               out_dtype: torch.dtype) -> torch.Tensor:
-    """``rmsnorm`` written directly in ``out_dtype`` (e.g. fp32 residual -> bf16 activations)."""
-    if out_dtype == x.dtype:
+               out_dtype: torch.dtype, dw_acc: torch.Tensor | None = None) -> torch.Tensor:
+    """``rmsnorm`` written directly in ``out_dtype`` (e.g. fp32 residual -> bf16 activations);
+    ``dw_acc`` as for ``add_rmsnorm``."""
+    if out_dtype == x.dtype and dw_acc is None:
         return rmsnorm(x, weight, eps)
-    return _RMSNormTo.apply(x, weight, eps, out_dtype)
+    return _RMSNormTo.apply(x, weight, eps, out_dtype, dw_acc)

@@ -16,7 +16,8 @@ Every ``nn.Parameter`` of the model becomes a view into the master buffer
 The compute-dtype copy is what torch's autocast computes on the fly (each
 fp32 weight rounded to bf16 once per autocast region); here it is one cast
 kernel over the whole buffer, run by ``refresh`` -- by the model on every
-forward, or once per step inside ``hold()``.
+forward, or once per step inside ``hold()`` unless the optimizer already
+wrote it with the update (``mark_fresh``).
 """
 
 from __future__ import annotations
@@ -78,7 +79,8 @@ class FlatParams:
         self._shadow: dict[torch.dtype, torch.Tensor] = {}
         self._cache: dict[tuple, torch.Tensor] = {}
         self._held = False
-        self.refreshes = 0  # number of compute-copy refreshes (host-side counter)
+        self._fresh: set[torch.dtype] = set()  # copies known to equal the master weights
+        self.refreshes = 0  # number of compute-copy rewrites (host-side counter)
 
     # ------------------------------------------------------------ views
     def _view(self, buf: torch.Tensor, p: nn.Parameter) -> torch.Tensor:
@@ -135,14 +137,26 @@ class FlatParams:
             return False
         with torch.no_grad():
             self._shadow_buf(dtype).copy_(self.master)
-        self.refreshes += 1
+        self.mark_fresh(dtype)
         return True
+
+    def mark_fresh(self, dtype: torch.dtype) -> None:
+        """The ``dtype`` copy was just rewritten from the master weights (by ``refresh``
+        or by an optimizer step that writes it)."""
+        self._fresh = {dtype}
+        self.refreshes += 1
+
+    def invalidate(self) -> None:
+        """The master weights were changed outside the optimizer: the next ``hold``
+        refreshes the copy."""
+        self._fresh = set()
 
     @contextlib.contextmanager
     def hold(self, dtype: torch.dtype):
-        """Refresh once, then keep the copy for every forward inside the block
-        (the master weights must not change inside it)."""
-        self.refresh(dtype)
+        """Refresh the copy unless it is known fresh, then keep it for every forward
+        inside the block (the master weights must not change inside it)."""
+        if dtype not in self._fresh:
+            self.refresh(dtype)
         self._held = dtype != torch.float32
         try:
             yield

@@ -153,12 +153,13 @@ class LlamaDecoderLayer(nn.Module):
         """(new residual, MLP output still to be added): the previous layer's MLP
         output ``pending`` is added inside this layer's first norm."""
         eps = self.input_layernorm.eps
+        w1, w2 = self.input_layernorm.weight, self.post_attention_layernorm.weight
         if pending is None:
-            x = rmsnorm_to(hidden, self.input_layernorm.weight, eps, dt)
+            x = rmsnorm_to(hidden, w1, eps, dt, dw_acc=flat.grad_of([w1]))
         else:
-            hidden, x = add_rmsnorm(hidden, pending, self.input_layernorm.weight, eps, dt)
+            hidden, x = add_rmsnorm(hidden, pending, w1, eps, dt, dw_acc=flat.grad_of([w1]))
         a = self.self_attn.fused(x, cos, sin, doc_ids, block_mask, flat, dt)
-        hidden, x = add_rmsnorm(hidden, a, self.post_attention_layernorm.weight, eps, dt)
+        hidden, x = add_rmsnorm(hidden, a, w2, eps, dt, dw_acc=flat.grad_of([w2]))
         return hidden, self.mlp.fused(x, flat, dt)
 
 
@@ -217,7 +218,8 @@ class LlamaForCausalLM(nn.Module):
             pending = None
             for layer in self.layers:
                 hidden, pending = layer.fused(hidden, pending, cos, sin, doc_ids, block_mask, flat, dt)
-            _, y = add_rmsnorm(hidden, pending, self.norm.weight, self.norm.eps, dt)
+            _, y = add_rmsnorm(hidden, pending, self.norm.weight, self.norm.eps, dt,
+                               dw_acc=flat.grad_of([self.norm.weight]))
             kw = dict(ignore_index=-100, z_loss_coeff=self.cfg.z_loss_coeff)
             if dt == torch.float32 or self.cfg.d_model % 8:
                 return linear_cross_entropy(y, self.embed_tokens.weight, labels,

@@ -6,10 +6,11 @@ the forward and ``(loss / step_tokens).backward()`` under bf16 autocast; then
 ``clip_grad_norm_(1.0)`` and a fused AdamW step.
 
 The parameters live in the model's flat store (``FlatParams``): the step
-zeroes the one gradient buffer, rounds the master weights to bf16 once for
-all micro-batches (``hold``), and clips and updates the one flat parameter --
-the same AdamW arithmetic as over the per-tensor list (uniform
-hyper-parameters, element-wise update), in a single fused launch.
+zeroes the one gradient buffer, runs every micro-batch on one bf16 copy of
+the weights (``hold``), and clips and updates the flat buffer with the fused
+``FlatAdamW`` -- the same arithmetic as ``clip_grad_norm_`` plus fused AdamW
+over the per-tensor list (uniform hyper-parameters, element-wise update) --
+whose update also writes the next step's bf16 copy.
 
 ``capture`` records that whole sequence once into a HIP graph on static
 device buffers (every hot-path op is capture-safe: no host synchronisation,
@@ -26,6 +27,7 @@ import torch
 
 from packbalance_amd.model.attention import build_doc_block_mask
 from packbalance_amd.model.llama import LlamaForCausalLM
+from packbalance_amd.model.optim import FlatAdamW
 
 
 class TrainStep:
@@ -37,8 +39,8 @@ class TrainStep:
         self.model = LlamaForCausalLM(cfg).to(dev)
         self.model.train()
         self.flat = self.model.flat_parameters()
-        self.opt = torch.optim.AdamW([self.flat.param], lr=lr, betas=(0.9, 0.95),
-                                     weight_decay=0.1, fused=True, capturable=True)
+        self.opt = FlatAdamW(self.flat, lr=lr, betas=(0.9, 0.95), weight_decay=0.1,
+                             max_grad_norm=1.0, copy_dtype=torch.bfloat16)
 
         def z():
             return torch.zeros((1, seq_len), dtype=torch.int64, device=dev)
@@ -61,9 +63,7 @@ class TrainStep:
                                   block_mask=bm)
                 (loss / step_tokens).backward()
                 self.loss_sum += loss.detach()
-        norm = torch.nn.utils.clip_grad_norm_([self.flat.param], 1.0)
-        self.grad_norm.copy_(norm)
-        self.opt.step()
+        self.grad_norm.copy_(self.opt.step())
 
     @staticmethod
     def _as_dicts(batch_list):

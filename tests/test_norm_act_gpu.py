@@ -257,3 +257,38 @@ def test_rmsnorm_to_bf16_matches_oracle(dev) -> None:
     _close(y, y_ref, 1e-2, "y")
     _close(xr.grad, dx_ref, 1e-5, "dx")
     _close(wr.grad, dw_ref, 1e-4, "dw")
+
+
+@pytest.mark.parametrize("rows,n", [(2048, 768), (40, 4096), (0, 768)])
+def test_norm_weight_grad_accumulates_into_fp32_buffer(rows, n, dev) -> None:
+    """dw_acc: the weight gradient is ADDED to a caller's fp32 buffer (the flat
+    store's slice) and None is returned for the weight; the increase equals the dw
+    the non-accumulating call returns (same kernel, same reduction order), and an
+    empty batch leaves the buffer unchanged."""
+    from packbalance_amd.kernels.rmsnorm import add_rmsnorm, rmsnorm_to
+
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(rows, n, generator=g).to(dev)
+    d = torch.randn(rows, n, generator=g).to(dev, torch.bfloat16)
+    w = (torch.randn(n, generator=g) * 0.1 + 1.0).to(dev)
+    dy = torch.randn(rows, n, generator=g).to(dev, torch.bfloat16)
+    acc0 = torch.randn(n, generator=g).to(dev)
+    for fused in (True, False):
+        wr = w.clone().requires_grad_(True)
+        wa = w.clone().requires_grad_(True)
+        acc = acc0.clone()
+        if fused:
+            _, y = add_rmsnorm(x, d, wr, 1e-5, torch.bfloat16)
+            _, ya = add_rmsnorm(x, d, wa, 1e-5, torch.bfloat16, dw_acc=acc)
+        else:
+            y = rmsnorm_to(x, wr, 1e-5, torch.bfloat16)
+            ya = rmsnorm_to(x, wa, 1e-5, torch.bfloat16, dw_acc=acc)
+        if rows == 0:
+            assert wa.grad is None
+            continue
+        y.backward(dy)
+        ya.backward(dy)
+        assert wa.grad is None
+        torch.testing.assert_close(acc - acc0, wr.grad, rtol=1e-5, atol=1e-4)
+    with pytest.raises(ValueError):
+        add_rmsnorm(x, d, w.to(torch.bfloat16), 1e-5, dw_acc=acc0)

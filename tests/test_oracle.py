@@ -18,6 +18,7 @@ import torch.nn.functional as F
 from oracle import attention as OA
 from oracle import block_mask as OB
 from oracle import kernels as OK
+from oracle import optim as OO
 
 GOLDEN = Path(__file__).resolve().parent / "golden" / "block_masks.npz"
 
@@ -280,3 +281,32 @@ def test_block_mask_dense_and_closed_agree(seed: int) -> None:
 def test_block_mask_rejects_batch() -> None:
     with pytest.raises(ValueError):
         OB.build_doc_block_tables(np.zeros((2, 8), dtype=np.int64), 1)
+
+
+# ---------------------------------------------------------------- clip + AdamW
+@pytest.mark.parametrize("max_norm", [1.0, 0.0, 50.0])
+def test_clip_adamw_oracle_matches_torch(max_norm) -> None:
+    """Five steps against torch's own clip_grad_norm_ + AdamW (float64, single-tensor
+    path); grads are scaled so clipping is active on some steps and not on others."""
+    rng = np.random.default_rng(0)
+    n = 1001
+    p0 = rng.standard_normal(n) * 0.02
+    tp = torch.nn.Parameter(torch.tensor(p0.copy()))
+    opt = torch.optim.AdamW([tp], lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1,
+                            foreach=False, fused=False)
+    p, m, v = p0.copy(), np.zeros(n), np.zeros(n)
+    step = 0
+    for k in range(5):
+        g = rng.standard_normal(n) * (0.01 if k % 2 else 0.2)
+        tp.grad = torch.tensor(g.copy())
+        tnorm = float(torch.nn.utils.clip_grad_norm_([tp], max_norm)) if max_norm > 0 else \
+            float(tp.grad.norm())
+        opt.step()
+        step, norm = OO.clip_adamw_step(p, g, m, v, step, lr=3e-4, betas=(0.9, 0.95), eps=1e-8,
+                                        weight_decay=0.1, max_norm=max_norm)
+        assert step == k + 1
+        assert abs(norm - tnorm) <= 1e-12 * tnorm
+        np.testing.assert_allclose(p, tp.detach().numpy(), rtol=1e-12, atol=1e-15)
+        st = opt.state[tp]
+        np.testing.assert_allclose(m, st["exp_avg"].numpy(), rtol=1e-12, atol=1e-18)
+        np.testing.assert_allclose(v, st["exp_avg_sq"].numpy(), rtol=1e-12, atol=1e-20)
