@@ -201,14 +201,15 @@ def attention_kernels(dev, iters: int) -> dict:
     dk = torch.empty(B, S, Hkv, D, device=dev, dtype=torch.bfloat16).transpose(1, 2)
     dv = torch.empty_like(dk)
     ws = torch.empty(plans["workspace"], dtype=torch.uint8, device=dev)
+    fws = torch.empty(max(1, plans["fwd_workspace"]), dtype=torch.uint8, device=dev)
     sc = 1.0 / D ** 0.5
     st = N.stream_ptr(q)
     pf, pq, pk = plans[A.FWD], plans[A.BWD_Q], plans[A.BWD_KV]
 
     def fwd():
         N.call("pb_attn_fwd", N.BHSD.of(q), N.BHSD.of(k), N.BHSD.of(v), N.BHSD.of(out),
-               lse.data_ptr(), doc.data_ptr(), doc.stride(0), pf.counts.data_ptr(),
-               pf.lists.data_ptr(), B, Hq, Hkv, S, D, sc, N.PB_BF16, st)
+               lse.data_ptr(), fws.data_ptr(), doc.data_ptr(), doc.stride(0),
+               pf.counts.data_ptr(), pf.lists.data_ptr(), B, Hq, Hkv, S, D, sc, N.PB_BF16, st)
 
     def bwd():
         N.call("pb_attn_bwd", N.BHSD.of(q), N.BHSD.of(k), N.BHSD.of(v), N.BHSD.of(out),

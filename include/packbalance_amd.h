@@ -144,10 +144,11 @@ typedef struct pb_bhsd {
 } pb_bhsd;
 
 /* Launch configuration of the attention kernels for one problem shape (no
- * reference counterpart).  out[0..7] = forward query tile, forward KV tile,
+ * reference counterpart).  out[0..9] = forward query tile, forward KV tile,
  * dK/dV query tile, dK/dV KV tile, dQ query tile, dQ KV tile, pb_attn_bwd
- * workspace bytes, dK/dV head-split flag.  Plans passed to pb_attn_fwd /
- * pb_attn_bwd must be built with these tile sizes.                          */
+ * workspace bytes, dK/dV head-split flag, pb_attn_fwd workspace bytes,
+ * forward KV chunk (KV tiles per workgroup; 0 = whole lists).  Plans passed
+ * to pb_attn_fwd / pb_attn_bwd must be built with these tile sizes.         */
 int pb_attn_config(int64_t b, int64_t hq, int64_t hkv, int64_t s, int64_t d, int64_t *out);
 
 /* Tile plan of a packed batch (no counterpart table in the reference; it is
@@ -168,9 +169,10 @@ int pb_attn_plan(const int64_t *doc_ids, int64_t doc_stride, int64_t b, int64_t 
  * q/k/v/out are bf16 (dtype must be PB_BF16), head_dim d <= 128, scale > 0.
  * lse (fp32 [b, hq, s]) receives log2(sum_j exp2(scale*log2(e)*q.k)) for the
  * backward.  plan = pb_attn_plan(by_kv = 0) with the forward tiles of
- * pb_attn_config.                                                           */
+ * pb_attn_config; workspace: out[8] bytes of pb_attn_config (may be NULL when
+ * that is 0).                                                               */
 int pb_attn_fwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v, const pb_bhsd *out,
-                float *lse, const int64_t *doc_ids, int64_t doc_stride,
+                float *lse, void *workspace, const int64_t *doc_ids, int64_t doc_stride,
                 const int32_t *plan_counts, const int32_t *plan_lists, int64_t b,
                 int64_t hq, int64_t hkv, int64_t s, int64_t d, float scale, int dtype,
                 void *stream);

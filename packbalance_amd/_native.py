@@ -74,7 +74,8 @@ SIGNATURES: dict[str, tuple] = {
     "pb_attn_plan": (_i32, [_p, _i64, _i64, _i64, _i64, _i64, _i32, _p, _p, _p, _p]),
     "pb_attn_fwd": (
         _i32,
-        [_pv, _pv, _pv, _pv, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _p],
+        [_pv, _pv, _pv, _pv, _p, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _i32,
+         _p],
     ),
     "pb_attn_bwd": (
         _i32,

@@ -52,6 +52,10 @@ struct BwdArgs {
   const int32_t *qcnt, *qlist;  // dQ plan (by query tile)
   const int32_t *kcnt, *klist;  // dK/dV plan (by KV tile)
   float *dk_part, *dv_part;     // split: fp32 [B][Hq][S][D] partials
+  // dQ KV split: KV tiles per workgroup (0: whole list), unscaled fp32 dQ
+  // partials [split][B][Hq][S][D] of query tiles with more than one chunk.
+  int dq_chunk;
+  float *dq_part;
   int B, Hq, Hkv, S, D;
   int nqt_dq, nkt_dq, nqt_kv, nkt_kv;
   float sl2, scale;
@@ -737,7 +741,21 @@ void attn_bwd_dq_pipe(BwdArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hh = lane >> 5, l32 = lane & 31;
   int qt, b, h;
-  decode_q_major((int)blockIdx.x, a.nqt_dq, a.B, a.Hq, a.Hkv, qt, b, h);
+  // Workgroup = (KV chunk, then the q-major order of the unsplit launch);
+  // unused chunk slots exit at once.
+  const int nbase = a.nqt_dq * a.B * a.Hq;
+  const int split = (int)blockIdx.x / nbase;
+  decode_q_major((int)blockIdx.x - split * nbase, a.nqt_dq, a.B, a.Hq, a.Hkv, qt, b, h);
+  const int cnt_all = a.qcnt[b * a.nqt_dq + qt];
+  int e_begin = 0, cnt = cnt_all;
+  bool part = false;
+  if (a.dq_chunk > 0) {
+    const int nch = (cnt_all + a.dq_chunk - 1) / a.dq_chunk;
+    if (split >= (nch > 0 ? nch : 1)) return;  // uniform over the workgroup
+    e_begin = split * a.dq_chunk;
+    cnt = min(a.dq_chunk, cnt_all - e_begin);
+    part = nch > 1;
+  }
   const int hk = h / (a.Hq / a.Hkv);
   const int S = a.S;
   const int64_t *docb = a.doc + b * a.doc_sb;
@@ -765,7 +783,7 @@ void attn_bwd_dq_pipe(BwdArgs a) {
       for (int i = 0; i < 8; ++i) dlt += (float)gf[dk][i] * (float)of[i];
     }
     dlt = xor32_sum(dlt);  // the lane halves hold complementary slices of the row
-    if (qvalid && hh == 0) a.delta[row_o] = dlt;
+    if (qvalid && hh == 0 && split == 0) a.delta[row_o] = dlt;
   }
   f32x16_t dq_acc[NDB];
 #pragma unroll
@@ -804,9 +822,8 @@ void attn_bwd_dq_pipe(BwdArgs a) {
     return *reinterpret_cast<bf16x8_t *>(&r);
   };
 
-  const int cnt = a.qcnt[b * a.nqt_dq + qt];
   const int U = 2 * cnt;
-  const int32_t *lst = a.qlist + ((int64_t)b * a.nqt_dq + qt) * a.nkt_dq;
+  const int32_t *lst = a.qlist + ((int64_t)b * a.nqt_dq + qt) * a.nkt_dq + e_begin;
   auto entry = [&](int u) { return lst[(u < U ? u : U - 1) >> 1]; };
   auto row0 = [&](int e, int u) { return plan_tile(e) * kKvStep + 32 * (u & 1); };
   // (The row is passed in, not computed here: calling another lambda inside
@@ -922,6 +939,22 @@ void attn_bwd_dq_pipe(BwdArgs a) {
   }
 
   if (!qvalid) return;
+  if (part) {
+    // This chunk's unscaled dQ rows, fp32 (summed and scaled by attn_bwd_dq_reduce).
+    const int64_t prow = (((int64_t)split * a.B + b) * a.Hq + h) * S + qi;
+    float *pq = a.dq_part + prow * DP;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq) {
+        typedef float f32x4_t __attribute__((ext_vector_type(4)));
+        f32x4_t o4;
+#pragma unroll
+        for (int x = 0; x < 4; ++x) o4[x] = dq_acc[db][4 * jq + x];
+        *reinterpret_cast<f32x4_t *>(pq + 32 * db + 8 * jq + 4 * hh) = o4;
+      }
+    return;
+  }
   bf16_t *qrow = a.dq.row(b, h, qi);
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
@@ -933,6 +966,34 @@ void attn_bwd_dq_pipe(BwdArgs a) {
       for (int x = 0; x < 4; ++x) o4[x] = (bf16_t)(dq_acc[db][4 * jq + x] * a.scale);
       *reinterpret_cast<bf16x4_t *>(qrow + 32 * db + 8 * jq + 4 * hh) = o4;
     }
+}
+
+// dQ of split query tiles = scale * sum of the chunk partials (bf16): DP/4
+// threads per (pack, head, query row), four elements each; rows of unsplit
+// tiles were written by attn_bwd_dq_pipe and are skipped.
+template <int DP>
+__global__ __launch_bounds__(256) void attn_bwd_dq_reduce(BwdArgs a, int bm) {
+  constexpr int TPR = DP / 4, RPB = 256 / TPR;
+  typedef float f32x4_t __attribute__((ext_vector_type(4)));
+  const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / TPR;
+  const int d0 = (threadIdx.x % TPR) * 4;
+  const int64_t rows = (int64_t)a.B * a.Hq * a.S;
+  if (row >= rows) return;
+  const int q = (int)(row % a.S);
+  const int64_t bh = row / a.S;
+  const int h = (int)(bh % a.Hq), b = (int)(bh / a.Hq);
+  const int cnt = a.qcnt[b * a.nqt_dq + q / bm];
+  const int nch = (cnt + a.dq_chunk - 1) / a.dq_chunk;
+  if (nch <= 1) return;
+  const float *pq = a.dq_part + row * DP + d0;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+  for (int c = 0; c < nch; ++c) acc += *reinterpret_cast<const f32x4_t *>(pq + c * rows * DP);
+  typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+  bf16x4_t o4;
+#pragma unroll
+  for (int x = 0; x < 4; ++x) o4[x] = (bf16_t)(acc[x] * a.scale);
+  *reinterpret_cast<bf16x4_t *>(a.dq.row(b, h, q) + d0) = o4;
 }
 
 // Two entry points over one body: two waves per SIMD (so one wave's softmax
@@ -977,6 +1038,8 @@ extern "C" int pb_attn_config(int64_t b, int64_t hq, int64_t hkv, int64_t s, int
   out[5] = kKvStep;
   out[6] = attn_bwd_workspace(b, hq, hkv, s, d);
   out[7] = c.split;
+  out[8] = attn_fwd_workspace(b, hq, hkv, s, d);
+  out[9] = c.fwd_chunk;
   return PB_OK;
 }
 
@@ -1007,6 +1070,8 @@ extern "C" int pb_attn_bwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v,
   const int64_t delta_bytes = (b * hq * s * 4 + 255) / 256 * 256;
   a.dk_part = reinterpret_cast<float *>(ws + delta_bytes);
   a.dv_part = a.dk_part + b * hq * s * d;
+  a.dq_chunk = 0;
+  a.dq_part = reinterpret_cast<float *>(ws + attn_bwd_dq_part_offset(b, hq, s, d, cfg.split != 0));
   a.doc = doc_ids;
   a.doc_sb = doc_stride;
   a.qcnt = q_plan_counts; a.qlist = q_plan_lists;
@@ -1040,6 +1105,10 @@ extern "C" int pb_attn_bwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v,
                     (reinterpret_cast<uintptr_t>(workspace) & 15) == 0 &&
                     32 * std::max({q->stride_s, dout->stride_s, k->stride_s, v->stride_s}) <
                         (1LL << 30);
+  if (pipe && cfg.dq_chunk > 0) {
+    a.dq_chunk = cfg.dq_chunk;
+    g_q.x *= (unsigned)cfg.dq_splits;
+  }
   if (pipe) {
 #define PB_DQP(DP, W) hipLaunchKernelGGL((attn_bwd_dq_pipe<DP, W>), g_q, dim3(64 * W), 0, st, a)
     if (cfg.dq_waves == 4) { if (d == 128) PB_DQP(128, 4); else PB_DQP(64, 4); }
@@ -1067,6 +1136,12 @@ extern "C" int pb_attn_bwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v,
   if (cfg.split) {
     const int64_t n = b * hkv * s * d;
     hipLaunchKernelGGL(attn_bwd_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a);
+  }
+  if (a.dq_chunk > 0) {
+    const int64_t rows = b * hq * s, rpb = 256 / (d / 4);
+    const dim3 rgrid((unsigned)((rows + rpb - 1) / rpb));
+    if (d == 128) hipLaunchKernelGGL(attn_bwd_dq_reduce<128>, rgrid, dim3(256), 0, st, a, cfg.dq_q_tile());
+    else hipLaunchKernelGGL(attn_bwd_dq_reduce<64>, rgrid, dim3(256), 0, st, a, cfg.dq_q_tile());
   }
   return launch_status("pb_attn_bwd");
 }

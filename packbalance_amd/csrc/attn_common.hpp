@@ -262,8 +262,18 @@ inline bool views_vectorizable(int64_t d, std::initializer_list<const pb_bhsd *>
 // only 12 heads x 16 query tiles).  When even that leaves the dK/dV grid
 // short, every query head of a GQA group gets its own workgroup and writes an
 // fp32 partial that a small kernel sums (split).
+//
+// Forward KV split: a packed pack holds a few long documents, so the KV list
+// of a late query tile can be 10-30 tiles long while the average is a third
+// of that; on a small grid the longest list sets the kernel time.  When the
+// grid is small, each query tile's list is cut into chunks of fwd_chunk KV
+// tiles, one workgroup per chunk (fwd_splits = most chunks any list can
+// need); a tile with more than one chunk leaves normalised fp32 partial
+// outputs and their log-sum-exps, merged by a combine kernel.
 struct AttnConfig {
   int fwd_waves, dq_waves, kv_waves, split;
+  int fwd_chunk, fwd_splits;  // 0 / 1: no forward KV split
+  int dq_chunk, dq_splits;    // the same for the (q-major) dQ kernel
   int fwd_q_tile() const { return 32 * fwd_waves; }
   int dq_q_tile() const { return 32 * dq_waves; }
   int kv_tile() const { return 32 * kv_waves; }
@@ -279,16 +289,47 @@ inline AttnConfig attn_config(int64_t b, int64_t hq, int64_t hkv, int64_t s, int
   c.dq_waves = big_q ? 4 : 2;
   c.kv_waves = b * hkv * tiles(128) >= kFill ? 4 : 2;
   c.split = (c.kv_waves == 2 && b * hkv * tiles(64) < kFill && hq > hkv) ? 1 : 0;
+  // Aim for ~4096 chunk workgroups over all lists, but at least 4 KV tiles
+  // each (a chunk also pays the prologue and the merge).
+  auto kv_split = [&](int64_t q_rows, int &chunk_out, int &splits_out) {
+    chunk_out = 0;
+    splits_out = 1;
+    const int64_t base = b * hq * tiles((int)q_rows), nkt = tiles(64);
+    if (base >= 4 * kFill) return;
+    int64_t chunk = (nkt * base + 4095) / 4096;
+    if (chunk < 4) chunk = 4;
+    if (chunk < nkt) {
+      chunk_out = (int)chunk;
+      splits_out = (int)((nkt + chunk - 1) / chunk);
+    }
+  };
+  kv_split(c.fwd_q_tile(), c.fwd_chunk, c.fwd_splits);
+  kv_split(c.dq_q_tile(), c.dq_chunk, c.dq_splits);
   return c;
 }
 
+// Workspace of pb_attn_fwd: with a KV split, the partial outputs
+// [splits, b, hq, s, d] and log-sum-exps [splits, b, hq, s], fp32.
+inline int64_t attn_fwd_workspace(int64_t b, int64_t hq, int64_t hkv, int64_t s, int64_t d) {
+  const AttnConfig c = attn_config(b, hq, hkv, s, d);
+  if (c.fwd_chunk == 0) return 0;
+  const int64_t rows = (int64_t)c.fwd_splits * b * hq * s;
+  return (rows * d * 4 + 255) / 256 * 256 + (rows * 4 + 255) / 256 * 256;
+}
+
 // Workspace of pb_attn_bwd: delta [b, hq, s] fp32, then (split) dK and dV
-// partials [b, hq, s, d] fp32 each.
+// partials [b, hq, s, d] fp32 each, then (dQ KV split) dQ partials
+// [dq_splits, b, hq, s, d] fp32.
+inline int64_t attn_bwd_dq_part_offset(int64_t b, int64_t hq, int64_t s, int64_t d, bool split) {
+  int64_t bytes = (b * hq * s * 4 + 255) / 256 * 256;
+  if (split) bytes += 2 * b * hq * s * d * 4;
+  return bytes;
+}
+
 inline int64_t attn_bwd_workspace(int64_t b, int64_t hq, int64_t hkv, int64_t s, int64_t d) {
   const AttnConfig c = attn_config(b, hq, hkv, s, d);
-  int64_t bytes = b * hq * s * 4;
-  bytes = (bytes + 255) / 256 * 256;
-  if (c.split) bytes += 2 * b * hq * s * d * 4;
+  int64_t bytes = attn_bwd_dq_part_offset(b, hq, s, d, c.split != 0);
+  if (c.dq_chunk) bytes += (int64_t)c.dq_splits * b * hq * s * d * 4;
   return bytes;
 }
 

@@ -9,6 +9,11 @@
 // from the grid size).  The workgroup walks only the KV tiles (64 rows) that
 // the tile plan lists for its query tile -- tiles with no same-document causal
 // pair are never loaded -- and applies the element mask only on PARTIAL tiles.
+// On small grids the pipelined kernel also splits each list into chunks of
+// fwd_chunk tiles (one workgroup each, attn_config); a query tile with more
+// than one chunk writes per-chunk fp32 outputs and log-sum-exps, and
+// attn_fwd_combine merges them (o = sum_c 2^(lse_c - lse) o_c,
+// lse = log2 sum_c 2^lse_c).
 //
 // Per KV tile a wave computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16, so a
 // lane owns one query column: the online-softmax max/sum are lane-local plus
@@ -48,6 +53,11 @@ struct FwdArgs {
   int B, Hq, Hkv, S, D, nqt, nkt;
   float sl2;  // softmax scale * log2(e)
   int vec;    // 16-byte global access allowed
+  // KV split (pipelined kernel): chunk = KV tiles per workgroup (0: whole
+  // list); bm = query rows per tile; partial outputs [split][B][Hq][S][D]
+  // and log-sum-exps [split][B][Hq][S], fp32.
+  int chunk, bm;
+  float *part_o, *part_lse;
 };
 
 // Generic path: any head dim <= 128, any strides / alignment (element-wise
@@ -286,7 +296,21 @@ void attn_fwd_pipe(FwdArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hh = lane >> 5, l32 = lane & 31;
   int qt, b, h;
-  decode_q_major((int)blockIdx.x, a.nqt, a.B, a.Hq, a.Hkv, qt, b, h);
+  // Workgroup = (KV chunk, then the q-major order of the unsplit launch): the
+  // first chunks of every list start first, unused chunk slots exit at once.
+  const int nbase = a.nqt * a.B * a.Hq;
+  const int split = (int)blockIdx.x / nbase;
+  decode_q_major((int)blockIdx.x - split * nbase, a.nqt, a.B, a.Hq, a.Hkv, qt, b, h);
+  const int cnt_all = a.cnt[b * a.nqt + qt];
+  int e_begin = 0, cnt = cnt_all;
+  bool part = false;
+  if (a.chunk > 0) {
+    const int nch = (cnt_all + a.chunk - 1) / a.chunk;
+    if (split >= (nch > 0 ? nch : 1)) return;  // uniform over the workgroup
+    e_begin = split * a.chunk;
+    cnt = min(a.chunk, cnt_all - e_begin);
+    part = nch > 1;
+  }
   const int hk = h / (a.Hq / a.Hkv);
   const int S = a.S;
   const char *Kb = reinterpret_cast<const char *>(a.k + b * a.k_sb + hk * a.k_sh);
@@ -359,9 +383,8 @@ void attn_fwd_pipe(FwdArgs a) {
     for (int db = 0; db < NDB; ++db) oacc[qb][db] = zero16();
   }
 
-  const int cnt = a.cnt[b * a.nqt + qt];
   const int U = 2 * cnt;  // 32-row sub-tiles
-  const int32_t *lst = a.list + ((int64_t)b * a.nqt + qt) * a.nkt;
+  const int32_t *lst = a.list + ((int64_t)b * a.nqt + qt) * a.nkt + e_begin;
   // Plan entry of sub-tile u (clamped to the last one).  Loaded one body
   // ahead and ahead of that body's DMA, so waiting for it never waits for
   // DMA (vmcnt counts in issue order).
@@ -579,6 +602,23 @@ void attn_fwd_pipe(FwdArgs a) {
     const float lsum = xor32_sum(l_run[qb]);
     const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
     if (!qv[qb]) continue;
+    if (part) {
+      // One chunk's normalised output and log-sum-exp, fp32.
+      const int64_t prow = (((int64_t)split * a.B + b) * a.Hq + h) * S + qi[qb];
+      float *po = a.part_o + prow * DP;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int jq = 0; jq < 4; ++jq) {
+          typedef float f32x4_t __attribute__((ext_vector_type(4)));
+          f32x4_t o4;
+#pragma unroll
+          for (int x = 0; x < 4; ++x) o4[x] = oacc[qb][db][4 * jq + x] * inv;
+          *reinterpret_cast<f32x4_t *>(po + 32 * db + 8 * jq + 4 * hh) = o4;
+        }
+      if (hh == 0) a.part_lse[prow] = lsum > 0.f ? m_run[qb] + fast_log2(lsum) : -INFINITY;
+      continue;
+    }
     bf16_t *orow = a.o + b * a.o_sb + (int64_t)qi[qb] * a.o_ss + h * a.o_sh;
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
@@ -596,13 +636,57 @@ void attn_fwd_pipe(FwdArgs a) {
   }
 }
 
+// Merge of the per-chunk outputs of split query tiles: DP/4 threads per
+// (pack, head, query row), four output elements each; rows of unsplit tiles
+// were written by the attention kernel and are skipped.  Pass 1 takes the
+// largest chunk log-sum-exp, pass 2 accumulates the 2^(lse_c - max)-weighted
+// chunk outputs with independent (unrolled) 16-byte loads.
+template <int DP>
+__global__ __launch_bounds__(256) void attn_fwd_combine(FwdArgs a) {
+  constexpr int TPR = DP / 4, RPB = 256 / TPR;
+  typedef float f32x4_t __attribute__((ext_vector_type(4)));
+  const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / TPR;
+  const int d0 = (threadIdx.x % TPR) * 4;
+  const int64_t rows = (int64_t)a.B * a.Hq * a.S;
+  if (row >= rows) return;
+  const int q = (int)(row % a.S);
+  const int64_t bh = row / a.S;
+  const int h = (int)(bh % a.Hq), b = (int)(bh / a.Hq);
+  const int cnt = a.cnt[b * a.nqt + q / a.bm];
+  const int nch = (cnt + a.chunk - 1) / a.chunk;
+  if (nch <= 1) return;
+  const float *pl = a.part_lse + row;
+  const float *po = a.part_o + row * DP + d0;
+  float mx = -INFINITY;
+#pragma unroll 4
+  for (int c = 0; c < nch; ++c) mx = fmaxf(mx, pl[c * rows]);
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  float den = 0.f;
+  if (mx != -INFINITY) {
+#pragma unroll 4
+    for (int c = 0; c < nch; ++c) {
+      const float w = fast_exp2(pl[c * rows] - mx);
+      const f32x4_t o = *reinterpret_cast<const f32x4_t *>(po + c * rows * DP);
+      den += w;
+      acc += w * o;
+    }
+  }
+  const float inv = den > 0.f ? 1.0f / den : 0.f;
+  typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+  bf16x4_t o4;
+#pragma unroll
+  for (int x = 0; x < 4; ++x) o4[x] = (bf16_t)(acc[x] * inv);
+  *reinterpret_cast<bf16x4_t *>(a.o + b * a.o_sb + (int64_t)q * a.o_ss + h * a.o_sh + d0) = o4;
+  if (d0 == 0) a.lse[row] = den > 0.f ? mx + fast_log2(den) : -INFINITY;
+}
+
 }  // namespace attn
 }  // namespace pb
 
 using pb::bf16_t;
 
 extern "C" int pb_attn_fwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v,
-                           const pb_bhsd *out, float *lse, const int64_t *doc_ids,
+                           const pb_bhsd *out, float *lse, void *workspace, const int64_t *doc_ids,
                            int64_t doc_stride, const int32_t *plan_counts,
                            const int32_t *plan_lists, int64_t b, int64_t hq, int64_t hkv,
                            int64_t s, int64_t d, float scale, int dtype, void *stream) {
@@ -634,12 +718,25 @@ extern "C" int pb_attn_fwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v,
   a.nkt = (int)((s + kKvStep - 1) / kKvStep);
   a.sl2 = scale * kLog2e;
   a.vec = views_vectorizable(d, {q, k, v, out});
+  a.chunk = 0;
+  a.bm = cfg.fwd_q_tile();
+  a.part_o = nullptr;
+  a.part_lse = nullptr;
   dim3 grid((unsigned)(a.nqt * b * hq));
   hipStream_t st = as_stream(stream);
   // DMA tile offsets are 32-bit: 64 rows of K / V must span < 2 GiB.
   const bool pipe = a.vec && (d == 64 || d == 128) && s % 64 == 0 &&
                     (reinterpret_cast<uintptr_t>(doc_ids) & 15) == 0 && doc_stride % 2 == 0 &&
                     64 * std::max(k->stride_s, v->stride_s) < (1LL << 30);
+  if (pipe && cfg.fwd_chunk > 0) {
+    PB_CHECK_ARG(workspace != nullptr, "pb_attn_fwd: workspace is required for this shape");
+    a.chunk = cfg.fwd_chunk;
+    const int64_t prow = (int64_t)cfg.fwd_splits * b * hq * s;
+    a.part_o = static_cast<float *>(workspace);
+    a.part_lse = reinterpret_cast<float *>(static_cast<char *>(workspace) +
+                                           (prow * d * 4 + 255) / 256 * 256);
+    grid.x *= (unsigned)cfg.fwd_splits;
+  }
   if (pipe) {
 #define PB_PIPE(DP, W) hipLaunchKernelGGL((attn_fwd_pipe<DP, 32, W>), grid, dim3(64 * W), 0, st, a)
     if (cfg.fwd_waves == 4) {
@@ -648,6 +745,14 @@ extern "C" int pb_attn_fwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v,
       if (d == 128) PB_PIPE(128, 2); else PB_PIPE(64, 2);
     }
 #undef PB_PIPE
+    if (a.chunk > 0) {
+      rc = launch_status("pb_attn_fwd");
+      if (rc) return rc;
+      const int64_t rows = b * hq * s, rpb = 256 / (d / 4);
+      const dim3 cgrid((unsigned)((rows + rpb - 1) / rpb));
+      if (d == 128) hipLaunchKernelGGL(attn_fwd_combine<128>, cgrid, dim3(256), 0, st, a);
+      else hipLaunchKernelGGL(attn_fwd_combine<64>, cgrid, dim3(256), 0, st, a);
+    }
   } else {
     // Generic kernel: 32 query rows per wave, same query tile as the plan.
     const int w = cfg.fwd_q_tile() / 32;

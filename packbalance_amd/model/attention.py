@@ -128,10 +128,11 @@ FWD, BWD_KV, BWD_Q = 0, 1, 2
 
 def attn_config(b: int, hq: int, hkv: int, s: int, d: int) -> dict:
     """Tile sizes / workspace the kernels use for this shape (``pb_attn_config``)."""
-    out = (ctypes.c_int64 * 8)()
+    out = (ctypes.c_int64 * 10)()
     N.call("pb_attn_config", b, hq, hkv, s, d, out)
     return {"tiles": {FWD: (out[0], out[1]), BWD_KV: (out[2], out[3]), BWD_Q: (out[4], out[5])},
-            "workspace": int(out[6]), "split": bool(out[7])}
+            "workspace": int(out[6]), "split": bool(out[7]), "fwd_workspace": int(out[8]),
+            "fwd_chunk": int(out[9])}
 
 
 class _Plan:
@@ -179,6 +180,7 @@ def _plans(doc: torch.Tensor, hq: int, hkv: int, head_dim: int, block_mask) -> d
     cfg = attn_config(b, hq, hkv, s, head_dim)
     plans = {k: _Plan(doc, k, *cfg["tiles"][k]) for k in (FWD, BWD_KV, BWD_Q)}
     plans["workspace"] = cfg["workspace"]
+    plans["fwd_workspace"] = cfg["fwd_workspace"]
     if cache is not None:
         cache[key] = plans
     return plans
@@ -193,8 +195,11 @@ class _DocAttention(torch.autograd.Function):
         out = out_mem.transpose(1, 2)
         lse = torch.empty((B, Hq, S), dtype=torch.float32, device=q.device)
         p = plans[FWD]
+        ws = None
+        if plans["fwd_workspace"]:
+            ws = torch.empty(plans["fwd_workspace"], dtype=torch.uint8, device=q.device)
         N.call("pb_attn_fwd", N.BHSD.of(q), N.BHSD.of(k), N.BHSD.of(v), N.BHSD.of(out),
-               lse.data_ptr(), doc.data_ptr(), doc.stride(0), p.counts.data_ptr(),
+               lse.data_ptr(), N.ptr(ws), doc.data_ptr(), doc.stride(0), p.counts.data_ptr(),
                p.lists.data_ptr(), B, Hq, Hkv, S, D, float(scale), N.PB_BF16, N.stream_ptr(q))
         ctx.save_for_backward(q, k, v, out, lse, doc)
         ctx.plans = plans

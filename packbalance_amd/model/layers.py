@@ -22,6 +22,17 @@ instead of a sum of separately rounded products.
 * ``embed``: the token embedding; its backward adds the gradient rows into
   the fp32 table gradient (index_add) instead of building a dense [V, d]
   gradient per micro-batch.
+
+The weight-gradient GEMMs are off the backward's critical path (nothing in
+the pass reads them), and at 2048 tokens per micro-batch each GEMM fills only
+part of the GPU, so inside a captured HIP graph they run on a side stream
+(``WGRAD_SIDE_STREAM``) and overlap the input-gradient chain.  Eagerly they
+stay on the caller's stream: there the step is bound by launch overhead and
+the cross-stream waits cost more than the overlap returns.  Each one keeps its operands alive until a
+join that an autograd final callback queues at the end of the backward pass;
+the callback runs on the stream that called ``backward()``, which then waits
+for the side stream -- so gradients are complete when ``backward()`` returns,
+eagerly or inside a captured HIP graph (where the wait becomes a graph edge).
 """
 
 from __future__ import annotations
@@ -33,12 +44,58 @@ from packbalance_amd import _native as N
 from packbalance_amd.model.rope import _rope
 
 
-def _accumulate_wgrad(g: torch.Tensor, dy: torch.Tensor, x: torch.Tensor) -> None:
-    """g (fp32 [N, K]) += dy^T x, with dy [T, N] and x [T, K] in the compute dtype."""
+WGRAD_SIDE_STREAM = True
+
+
+class _SideStream:
+    """A default-priority side stream per device for weight-gradient GEMMs."""
+
+    _by_device: dict[int, "_SideStream"] = {}
+
+    def __init__(self, dev: torch.device) -> None:
+        self.stream = torch.cuda.Stream(dev)
+        self.keep: list[torch.Tensor] = []
+        self.task = None  # autograd graph task whose end joins this stream
+
+    @classmethod
+    def of(cls, dev: torch.device) -> "_SideStream":
+        idx = dev.index if dev.index is not None else torch.cuda.current_device()
+        s = cls._by_device.get(idx)
+        if s is None:
+            s = cls._by_device[idx] = cls(torch.device("cuda", idx))
+        return s
+
+    def run(self, fn, *keep: torch.Tensor) -> None:
+        self.stream.wait_stream(torch.cuda.current_stream(self.stream.device))
+        with torch.cuda.stream(self.stream):
+            fn()
+        self.keep.extend(keep)
+        task = torch._C._current_graph_task_id()
+        if task != self.task:
+            self.task = task
+            torch.autograd.Variable._execution_engine.queue_callback(self.join)
+
+    def join(self) -> None:
+        torch.cuda.current_stream(self.stream.device).wait_stream(self.stream)
+        self.keep.clear()
+        self.task = None
+
+
+def _wgrad(g: torch.Tensor, dy: torch.Tensor, x: torch.Tensor) -> None:
     if dy.dtype == torch.float32:
         g.addmm_(dy.t(), x)
     else:
         torch.addmm(g, dy.t(), x, out_dtype=torch.float32, out=g)
+
+
+def _accumulate_wgrad(g: torch.Tensor, dy: torch.Tensor, x: torch.Tensor) -> None:
+    """g (fp32 [N, K]) += dy^T x, with dy [T, N] and x [T, K] in the compute dtype
+    (on the side stream during a backward pass, else inline)."""
+    if (WGRAD_SIDE_STREAM and dy.is_cuda and torch._C._current_graph_task_id() >= 0
+            and torch.cuda.is_current_stream_capturing()):
+        _SideStream.of(dy.device).run(lambda: _wgrad(g, dy, x), dy, x)
+    else:
+        _wgrad(g, dy, x)
 
 
 def _mm(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
