@@ -94,10 +94,16 @@ __device__ __forceinline__ void store_out(void *out, int dtype, int64_t idx, flo
     static_cast<f16_t *>(out)[idx] = (f16_t)v;
 }
 
+// kDlogits stages its bf16 tile [BM][TP] (vocab-major) in the operand LDS
+// after the main loop, so both dlogits layouts leave as 16-byte stores.
+constexpr int TP = BN + 8;  // staging row pitch (elements): 272 bytes
+static_assert(BM * TP * 2 <= 2 * BM * AP * 2, "staging tile must fit the operand LDS");
+
 template <int MODE>
 __global__ __launch_bounds__(256) void gemm_nt(GemmArgs g) {
-  __shared__ __align__(16) bf16_t As[BM * AP];
-  __shared__ __align__(16) bf16_t Bs[BN * AP];
+  __shared__ __align__(16) bf16_t smem[(BM + BN) * AP];
+  bf16_t *const As = smem;
+  bf16_t *const Bs = smem + BM * AP;
   __shared__ float red_m[2][BN], red_s[2][BN];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -207,6 +213,9 @@ __global__ __launch_bounds__(256) void gemm_nt(GemmArgs g) {
           red_s[wm][nl] = sm;
         }
       } else {
+        // dlogits of this lane's token into the staging tile (vocab-major);
+        // padding rows / columns (m >= M, n >= N) hold 0.
+        if (j == 0) __syncthreads();  // every wave is done with the operand LDS
         const float lse = nvalid ? g.lse[n] : 0.f;
         const float lse2 = lse * kLog2e;
         const float scale = valid ? (*g.grad_out) * (1.0f + 2.0f * g.z * lse) : 0.f;
@@ -214,24 +223,37 @@ __global__ __launch_bounds__(256) void gemm_nt(GemmArgs g) {
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int mb = 64 * wm + 32 * i + 8 * q + 4 * hh;  // 4 consecutive vocab rows
-            float v4[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int m = m0 + mb + r;
-              float gv = fast_exp2(acc[i][j][4 * q + r] * kLog2e - lse2) * scale;
-              if ((int64_t)(g.v0 + m) == t) gv -= one;
-              v4[r] = m < g.M ? gv : 0.f;
-              if (m < g.M && nvalid) g.dlt[(int64_t)m * g.ldlt + n] = (bf16_t)v4[r];
-            }
-            if (nvalid) {
-              bf16_t *dst = g.dl + (int64_t)n * g.ldl + m0 + mb;
-#pragma unroll
-              for (int r = 0; r < 4; ++r)
-                if (m0 + mb + r < g.M) dst[r] = (bf16_t)v4[r];
-            }
+          for (int r = 0; r < 16; ++r) {
+            const int ml = 64 * wm + 32 * i + 8 * (r >> 2) + 4 * hh + (r & 3);
+            const int m = m0 + ml;
+            float gv = fast_exp2(acc[i][j][r] * kLog2e - lse2) * scale;
+            if ((int64_t)(g.v0 + m) == t) gv -= one;
+            smem[ml * TP + nl] = (bf16_t)(m < g.M && nvalid ? gv : 0.f);
           }
+      }
+    }
+    if constexpr (MODE == kDlogits) {
+      __syncthreads();
+      // dL^T [vocab][tokens]: 16 threads per 256-byte staging row.
+#pragma unroll
+      for (int k = 0; k < BM * (BN / 8) / 256; ++k) {
+        const int c = tid + 256 * k;
+        const int ml = c >> 4, n8 = (c & 15) * 8;
+        if (m0 + ml < g.M && n0 + n8 < g.N)
+          *reinterpret_cast<u32x4 *>(g.dlt + (int64_t)(m0 + ml) * g.ldlt + n0 + n8) =
+              *reinterpret_cast<const u32x4 *>(&smem[ml * TP + n8]);
+      }
+      // dL [tokens][vocab]: lane <-> token (conflict-free column reads), eight
+      // vocab rows per 16-byte store.
+#pragma unroll
+      for (int k = 0; k < (BM / 8) * BN / 256; ++k) {
+        const int nl = tid & (BN - 1), m8 = 8 * ((tid >> 7) + 2 * k);
+        if (n0 + nl < g.N && m0 + m8 < g.M) {
+          bf16x8_t v;
+#pragma unroll
+          for (int x = 0; x < 8; ++x) v[x] = smem[(m8 + x) * TP + nl];
+          *reinterpret_cast<bf16x8_t *>(g.dl + (int64_t)(n0 + nl) * g.ldl + m0 + m8) = v;
+        }
       }
     }
     if constexpr (MODE == kLse) {
