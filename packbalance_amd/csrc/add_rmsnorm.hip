@@ -203,7 +203,7 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_bwd_reg(AddNormBwd a) {
 #pragma unroll 1
   for (int64_t row = r0 + wave; row < r1; row += kWaves) {
     const float r = a.rstd[row];
-    float hh[NV][8], g[NV][8];
+    float hh[NV][8], g[NV][8], dr[NV][8];
     float dot = 0.f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
@@ -212,6 +212,9 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_bwd_reg(AddNormBwd a) {
         float dy[8];
         ld8(a.h + (row * a.hs + c) * hb, a.hdt, hh[i], true);
         ld8(a.dy + (row * a.dys + c) * yb, a.dydt, dy, true);
+        // The incoming residual gradient does not depend on the row sum: load
+        // it with the rest so the row costs one memory round trip, not two.
+        if (a.dres) ld8(a.dres + (row * a.drs + c) * hb, a.hdt, dr[i], true);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           hh[i][e] *= r;
@@ -230,10 +233,8 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_bwd_reg(AddNormBwd a) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) d[e] = r * (g[i][e] - hh[i][e] * dot);
         if (a.dres) {
-          float dr[8];
-          ld8(a.dres + (row * a.drs + c) * hb, a.hdt, dr, true);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) d[e] += dr[e];
+          for (int e = 0; e < 8; ++e) d[e] += dr[i][e];
         }
         st8(a.dx + (row * a.dxs + c) * hb, a.hdt, d);
         if (a.ddelta) st8(a.ddelta + (row * a.dds + c) * db, a.dddt, d);
@@ -305,31 +306,32 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_bwd_loop(AddNormBwd a) {
 }
 
 // dw[c] = sum_p partial[p, c] in dtype wdt, or dw[c] += that sum (fp32 dw)
-// when accumulate is set.  A workgroup owns 16 columns; its 16 part-lanes
-// sum every 16th partial row (fixed order, so the result is deterministic)
-// and are folded in LDS.  Small column tiles keep n / 16 workgroups busy
-// on the few-hundred-row partial tables the backward leaves.
-constexpr int kRedCols = 16, kRedParts = 16;
-__global__ __launch_bounds__(kRedCols *kRedParts) void add_rmsnorm_dw_reduce(
+// when accumulate is set.  A workgroup of 16 waves owns 64 columns; wave w
+// sums partial rows w, w+16, ... with eight independent accumulators (eight
+// loads in flight per lane: the table is a few hundred rows and the kernel
+// is bound by load latency, not bandwidth), then the 16 wave sums are
+// folded in LDS in a fixed order, so the result is deterministic.
+constexpr int kRedWaves = 16;
+__global__ __launch_bounds__(64 * kRedWaves) void add_rmsnorm_dw_reduce(
     const float *__restrict__ partial, char *dw, int wdt, int nparts, int n, int accumulate) {
-  __shared__ float red[kRedParts][kRedCols];
-  const int cl = threadIdx.x % kRedCols, pl = threadIdx.x / kRedCols;
-  const int col = blockIdx.x * kRedCols + cl;
-  float s0 = 0.f, s1 = 0.f;
+  __shared__ float red[kRedWaves][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int col = blockIdx.x * 64 + lane;
+  float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (col < n) {
-    int p = pl;
-    for (; p + kRedParts < nparts; p += 2 * kRedParts) {
-      s0 += partial[(int64_t)p * n + col];
-      s1 += partial[(int64_t)(p + kRedParts) * n + col];
+    int p = w;
+    for (; p + 7 * kRedWaves < nparts; p += 8 * kRedWaves) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) s[k] += partial[(int64_t)(p + k * kRedWaves) * n + col];
     }
-    if (p < nparts) s0 += partial[(int64_t)p * n + col];
+    for (; p < nparts; p += kRedWaves) s[0] += partial[(int64_t)p * n + col];
   }
-  red[pl][cl] = s0 + s1;
+  red[w][lane] = ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
   __syncthreads();
-  if (pl == 0 && col < n) {
+  if (w == 0 && col < n) {
     float t = 0.f;
 #pragma unroll
-    for (int g = 0; g < kRedParts; ++g) t += red[g][cl];
+    for (int g = 0; g < kRedWaves; ++g) t += red[g][lane];
     if (accumulate)
       reinterpret_cast<float *>(dw)[col] += t;
     else
@@ -477,8 +479,8 @@ extern "C" int pb_add_rmsnorm_bwd(const void *dy, int64_t dy_row_stride, int dy_
   }
   int s = launch_status("pb_add_rmsnorm_bwd");
   if (s) return s;
-  hipLaunchKernelGGL(add_rmsnorm_dw_reduce, dim3((unsigned)((n + kRedCols - 1) / kRedCols)),
-                     dim3(kRedCols * kRedParts), 0, st, a.partial, static_cast<char *>(dw), w_dtype,
-                     nwg, (int)n, dw_accumulate ? 1 : 0);
+  hipLaunchKernelGGL(add_rmsnorm_dw_reduce, dim3((unsigned)((n + 63) / 64)), dim3(64 * kRedWaves),
+                     0, st, a.partial, static_cast<char *>(dw), w_dtype, nwg, (int)n,
+                     dw_accumulate ? 1 : 0);
   return launch_status("pb_add_rmsnorm_bwd(dw)");
 }
