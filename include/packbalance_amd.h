@@ -251,6 +251,26 @@ int pb_add_rmsnorm_bwd(const void *dy, int64_t dy_row_stride, int dy_dtype, cons
                        int ddelta_dtype, void *dw, int dw_accumulate, void *workspace,
                        int64_t rows, int64_t n, void *stream);
 
+/* ---- Model inputs of packs, built on the device --------------------------
+ * Replaces packbalance/data/dataset.py:33-76 (PackedDataset.__getitem__) for
+ * a batch of packs, reading a token store resident in device memory (the
+ * tokens.bin of data/store.py:12-56; store_elem_bytes 2 = uint16, 4 =
+ * uint32, 8 = int64).  Pack p's segments are (seg_start[i], seg_len[i]) for
+ * i in [pack_seg[p], pack_seg[p+1]) (at most max_segs <= 4096 per pack).
+ * Outputs int64 [n_packs, total], total = seq_len (rows == 0: packed, the
+ * segments back to back from position 0) or rows * seq_len (rows > 0:
+ * padded, segment i in row i and the whole row one document):
+ *   input_ids = tokens, labels = next token of the same segment (-100 on its
+ *   last token), position_ids = 0..len-1, doc_ids = segment index;
+ *   pad_token_id / -100 / 0 / -1 at every other position.
+ * The caller validates the table (segments inside the store, packs within
+ * total); the kernel keeps every access in bounds regardless.              */
+int pb_pack_tensors(const void *store, int store_elem_bytes, int64_t store_len,
+                    const int64_t *seg_start, const int64_t *seg_len, const int64_t *pack_seg,
+                    int64_t n_packs, int64_t max_segs, int64_t seq_len, int64_t rows,
+                    int64_t pad_token_id, int64_t *input_ids, int64_t *labels,
+                    int64_t *position_ids, int64_t *doc_ids, void *stream);
+
 /* ---- Clip-by-global-norm + AdamW over one flat fp32 buffer --------------
  * Replaces torch.nn.utils.clip_grad_norm_(params, max_grad_norm) followed by
  * torch.optim.AdamW(params, lr, (beta1, beta2), eps, weight_decay,

@@ -14,6 +14,7 @@ Modules (each function cites the reference file:line it follows):
               (torch.nn.attention.flex_attention.create_block_mask semantics)
   optim       gradient clipping + AdamW step (torch.nn.utils.clip_grad_norm_ +
               torch.optim.AdamW, as the reference's train loop calls them)
+  data        model inputs of packs from a token array (packbalance/data/dataset.py)
 
 How each function is pinned (beyond restating its formula) is listed in
 ``tests/test_oracle.py``; every oracle function has at least one check there

@@ -104,6 +104,10 @@ SIGNATURES: dict[str, tuple] = {
         [_p, _i64, _i32, _p, _i64, _i32, _p, _i32, _p, _p, _i64, _p, _i64, _p, _i64, _i32, _p, _i32,
          _p, _i64, _i64, _p],
     ),
+    "pb_pack_tensors": (
+        _i32,
+        [_p, _i32, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p],
+    ),
     "pb_clip_adamw_workspace_bytes": (_i64, [_i64]),
     "pb_clip_adamw_step": (
         _i32,

@@ -17,6 +17,7 @@ import torch.nn.functional as F
 
 from oracle import attention as OA
 from oracle import block_mask as OB
+from oracle import data as OD
 from oracle import kernels as OK
 from oracle import optim as OO
 
@@ -310,3 +311,50 @@ def test_clip_adamw_oracle_matches_torch(max_norm) -> None:
         st = opt.state[tp]
         np.testing.assert_allclose(m, st["exp_avg"].numpy(), rtol=1e-12, atol=1e-18)
         np.testing.assert_allclose(v, st["exp_avg_sq"].numpy(), rtol=1e-12, atol=1e-20)
+
+
+# ---------------------------------------------------------------- pack tensors
+def test_pack_tensors_oracle_known_answers() -> None:
+    """Worked by hand from dataset.py:33-76: two documents packed into 8 slots, and
+    the padded form with one document per 4-token row."""
+    tokens = np.array([10, 11, 12, 13, 14, 15, 16], dtype=np.uint32)
+    got = OD.pack_tensors(tokens, [[(0, 3), (4, 2)]], 8, pad_token_id=7)
+    assert got["input_ids"].tolist() == [[10, 11, 12, 14, 15, 7, 7, 7]]
+    assert got["labels"].tolist() == [[11, 12, -100, 15, -100, -100, -100, -100]]
+    assert got["position_ids"].tolist() == [[0, 1, 2, 0, 1, 0, 0, 0]]
+    assert got["doc_ids"].tolist() == [[0, 0, 0, 1, 1, -1, -1, -1]]
+    pad = OD.pack_tensors(tokens, [[(1, 3), (6, 1)]], 4, rows=2, pad_token_id=0)
+    assert pad["input_ids"].tolist() == [[11, 12, 13, 0, 16, 0, 0, 0]]
+    assert pad["labels"].tolist() == [[12, 13, -100, -100, -100, -100, -100, -100]]
+    assert pad["position_ids"].tolist() == [[0, 1, 2, 0, 0, 0, 0, 0]]
+    assert pad["doc_ids"].tolist() == [[0, 0, 0, 0, 1, 1, 1, 1]]
+    with pytest.raises(ValueError):
+        OD.pack_tensors(tokens, [[(0, 5), (0, 4)]], 8)
+
+
+def test_pack_tensors_oracle_reference_invariants() -> None:
+    """The checks of the reference's tests/test_dataset.py:17-42 on random packs."""
+    rng = np.random.default_rng(3)
+    tokens = rng.integers(0, 50000, size=5000).astype(np.uint32)
+    packs = []
+    for _ in range(6):
+        segs, used = [], 0
+        while True:
+            n = int(rng.integers(1, 120))
+            if used + n > 512:
+                break
+            segs.append((int(rng.integers(0, 5000 - n)), n))
+            used += n
+        packs.append(segs)
+    got = OD.pack_tensors(tokens, packs, 512)
+    for p, segs in enumerate(packs):
+        off = 0
+        for seg_id, (start, n) in enumerate(segs):
+            toks = tokens[start:start + n].astype(np.int64)
+            np.testing.assert_array_equal(got["input_ids"][p, off:off + n], toks)
+            np.testing.assert_array_equal(got["labels"][p, off:off + n - 1], toks[1:])
+            assert got["labels"][p, off + n - 1] == -100
+            np.testing.assert_array_equal(got["position_ids"][p, off:off + n], np.arange(n))
+            assert (got["doc_ids"][p, off:off + n] == seg_id).all()
+            off += n
+        assert (got["labels"][p, off:] == -100).all() and (got["doc_ids"][p, off:] == -1).all()
