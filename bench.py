@@ -5,7 +5,10 @@ Headline (``value``): useful tokens/s of the 100M Llama packed-2048 training
 step (4 packs of 2048 tokens per step, heavy-tail lognormal documents packed
 best-fit-decreasing, bf16 autocast with fp32 master weights, clip + fused
 AdamW) -- the semantics of the reference's ``profiling/bench_train.py:54-163``:
-useful tok/s = sum of pack tokens / sum of timed step seconds.
+useful tok/s = sum of pack tokens / sum of timed step seconds.  The corpus is a
+synthetic uint32 token store resident in HBM; each step's packs are built on
+the device from it (``pb_pack_tensors``) as the step's first work, the part
+of the reference's timed step that loads and copies its micro-batches.
 
 Kernel figures (HIP events around each C-ABI launch, on the stream the kernel
 runs on):
@@ -111,18 +114,30 @@ def train_step_bench(steps: int, warmup: int, dev, use_graph: bool = True):
     from packbalance_amd.model.llama import cfg2_model, count_parameters
     from packbalance_amd.model.step import TrainStep
 
+    from packbalance_amd.data.device_packs import DeviceTokenStore, build_pack_batch
+
     cfg = cfg2_model()
-    ts = TrainStep(cfg, dev)
     plan = W.cfg2_steps(warmup + steps)
+    # Synthetic corpus: every document of the run, uniform token ids, in one
+    # uint32 token store resident in HBM; each step's packs are (start, length)
+    # segments of it and are built on the device inside the step.
     rng = np.random.default_rng(0)
-    batches = [[W.pack_tensors([p], 2048, cfg.vocab_size, rng).to(dev) for p in st] for st in plan]
-    tokens = [torch.tensor(float(sum(b.useful_tokens for b in st)), device=dev) for st in batches]
+    n_tok = sum(n for st in plan for p in st for n in p)
+    store = DeviceTokenStore(rng.integers(0, cfg.vocab_size, size=n_tok).astype(np.uint32), dev)
+    step_packs, pos = [], 0
+    for st in plan:
+        packs = []
+        for p in st:
+            packs.append([(pos + sum(p[:i]), n) for i, n in enumerate(p)])
+            pos += sum(p)
+        step_packs.append(packs)
+    ts = TrainStep(cfg, dev, store=store)
     model = ts.model
     if use_graph:
-        ts.capture(batches[0], tokens[0])
-        run = lambda i: ts.replay(batches[i], tokens[i])  # noqa: E731
+        ts.capture_packs(step_packs[0])
+        run = lambda i: ts.replay_packs(step_packs[i])  # noqa: E731
     else:
-        run = lambda i: ts.eager(batches[i])  # noqa: E731
+        run = lambda i: ts.eager_packs(step_packs[i])  # noqa: E731
     for i in range(warmup):
         run(i)
     torch.cuda.synchronize()
@@ -131,10 +146,10 @@ def train_step_bench(steps: int, warmup: int, dev, use_graph: bool = True):
         run(i)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    useful = sum(b.useful_tokens for st in batches[warmup:] for b in st)
+    useful = sum(n for st in plan[warmup:] for p in st for n in p)
     from oracle.model import step_flops
 
-    flops = sum(step_flops(cfg, [b.doc_lengths[0] for b in st]) for st in batches[warmup:])
+    flops = sum(step_flops(cfg, st) for st in plan[warmup:])
     res = {
         "tok_s": useful / dt,
         "ms_per_step": dt / steps * 1e3,
@@ -142,8 +157,13 @@ def train_step_bench(steps: int, warmup: int, dev, use_graph: bool = True):
         "params": count_parameters(model),
         "model_tflops": flops / dt / 1e12,
         "hip_graph": use_graph,
+        "packs_built_on_device": True,
     }
-    return res, model, cfg, batches
+    # The first pack of the first timed step, on the host, for the CPU baseline.
+    first = build_pack_batch(store, [step_packs[warmup][0]], 2048)
+    cpu_pack = W.PackBatch(first["input_ids"].cpu(), first["labels"].cpu(),
+                           first["position_ids"].cpu(), first["doc_ids"].cpu(), [plan[warmup][0]])
+    return res, model, cfg, cpu_pack
 
 
 # ---------------------------------------------------------------- cpu baseline
@@ -424,8 +444,8 @@ def main() -> int:
         return 0
 
     log(f"train step: {args.warmup} warmup + {args.steps} timed steps")
-    train, model, cfg, batches = train_step_bench(args.steps, args.warmup, dev,
-                                                  use_graph=not args.eager)
+    train, model, cfg, cpu_pack = train_step_bench(args.steps, args.warmup, dev,
+                                                   use_graph=not args.eager)
     log(f"train: {train['tok_s']:.0f} tok/s, {train['ms_per_step']:.2f} ms/step")
     if args.only == "train":
         print(json.dumps({"train": train}), flush=True)
@@ -452,7 +472,7 @@ def main() -> int:
     base = None
     if not args.skip_cpu:
         log("cpu baseline (eager fp32 CPU path)")
-        base = cpu_baseline(model, cfg, batches[args.warmup][0])
+        base = cpu_baseline(model, cfg, cpu_pack)
 
     line = {
         "metric": "useful tok/s fwd+bwd (100M, 2048 packed); masked-attn TFLOP/s; CE GB/s",

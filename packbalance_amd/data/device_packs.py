@@ -165,7 +165,9 @@ class PackBuilder:
         cap = max_segments or n_packs * (rows or seq_len)
         self.cap = int(cap)
         dev = store.device
-        self._table = torch.zeros(2 * self.cap + n_packs + 1, dtype=torch.int64, device=dev)
+        # [starts (cap) | lengths (cap) | pack offsets (n_packs + 1) | useful tokens (1)]
+        self._table = torch.zeros(2 * self.cap + n_packs + 2, dtype=torch.int64, device=dev)
+        self.useful_count = self._table[-1]  # device int64: the step's document tokens
         self.outputs = _outputs(n_packs, rows * seq_len if rows else seq_len, dev)
         # The kernel bounds each pack's segment count by this (its LDS offsets);
         # a captured launch keeps it, so it is the builder's maximum, not a step's.
@@ -182,12 +184,13 @@ class PackBuilder:
         h = np.zeros(self._table.numel(), dtype=np.int64)
         h[:ns] = tab.seg_start
         h[self.cap:self.cap + ns] = tab.seg_len
-        h[2 * self.cap:] = tab.pack_seg
-        self._table.copy_(torch.from_numpy(h).pin_memory(), non_blocking=True)
+        h[2 * self.cap:2 * self.cap + self.n_packs + 1] = tab.pack_seg
         self.useful_tokens = int(tab.seg_len.sum())
+        h[-1] = self.useful_tokens
+        self._table.copy_(torch.from_numpy(h).pin_memory(), non_blocking=True)
 
     def launch(self) -> dict:
         t = self._table
-        _launch(self.store, t[:self.cap], t[self.cap:2 * self.cap], t[2 * self.cap:], self.n_packs,
-                self.max_segs, self.seq_len, self.rows, self.pad, self.outputs)
+        _launch(self.store, t[:self.cap], t[self.cap:2 * self.cap], t[2 * self.cap:-1],
+                self.n_packs, self.max_segs, self.seq_len, self.rows, self.pad, self.outputs)
         return self.outputs

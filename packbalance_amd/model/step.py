@@ -12,6 +12,13 @@ the weights (``hold``), and clips and updates the flat buffer with the fused
 over the per-tensor list (uniform hyper-parameters, element-wise update) --
 whose update also writes the next step's bf16 copy.
 
+With a ``DeviceTokenStore`` the step's packs are built on the device
+(``PackBuilder``: input ids, labels, positions and document ids from the
+store in HBM and a small per-step segment table) as the first work of the
+step -- the part of the reference's timed step that loads and copies the
+micro-batches (``bench_train.py:103-111``) -- and the step's token count
+comes from the same table, so a replay needs only the table's copy.
+
 ``capture`` records that whole sequence once into a HIP graph on static
 device buffers (every hot-path op is capture-safe: no host synchronisation,
 device-resident grad scale, all workspaces from the caching allocator);
@@ -25,6 +32,7 @@ from __future__ import annotations
 
 import torch
 
+from packbalance_amd.data.device_packs import DeviceTokenStore, PackBuilder
 from packbalance_amd.model.attention import build_doc_block_mask
 from packbalance_amd.model.llama import LlamaForCausalLM
 from packbalance_amd.model.optim import FlatAdamW
@@ -32,7 +40,7 @@ from packbalance_amd.model.optim import FlatAdamW
 
 class TrainStep:
     def __init__(self, cfg, dev, packs_per_step: int = 4, seq_len: int | None = None,
-                 seed: int = 0, lr: float = 3e-4):
+                 seed: int = 0, lr: float = 3e-4, store: DeviceTokenStore | None = None):
         self.cfg, self.dev = cfg, dev
         seq_len = seq_len or cfg.max_seq_len
         torch.manual_seed(seed)
@@ -45,14 +53,23 @@ class TrainStep:
         def z():
             return torch.zeros((1, seq_len), dtype=torch.int64, device=dev)
 
-        self.static = [dict(input_ids=z(), labels=z(), position_ids=z(), doc_ids=z())
-                       for _ in range(packs_per_step)]
+        self.builder = None
+        if store is not None:
+            self.builder = PackBuilder(store, packs_per_step, seq_len)
+            out = self.builder.outputs
+            self.static = [{k: out[k][i:i + 1] for k in out} for i in range(packs_per_step)]
+        else:
+            self.static = [dict(input_ids=z(), labels=z(), position_ids=z(), doc_ids=z())
+                           for _ in range(packs_per_step)]
         self.step_tokens = torch.ones((), dtype=torch.float32, device=dev)
         self.loss_sum = torch.zeros((), dtype=torch.float32, device=dev)
         self.grad_norm = torch.zeros((), dtype=torch.float32, device=dev)
         self.graph = None
 
-    def _body(self, batches, step_tokens) -> None:
+    def _body(self, batches, step_tokens, build: bool = False) -> None:
+        if build:  # the step's packs from the device token store
+            self.builder.launch()
+            self.step_tokens.copy_(self.builder.useful_count)
         self.loss_sum.zero_()
         self.flat.attach_grads()
         self.flat.zero_grad()
@@ -97,4 +114,26 @@ class TrainStep:
 
     def replay(self, batch_list, tokens_dev) -> None:
         self._load(batch_list, tokens_dev)
+        self.graph.replay()
+
+    # ---- packs built on the device (needs ``store``): packs are lists of
+    # (start, length) segments of the token store, one list per micro-batch.
+    def eager_packs(self, packs) -> None:
+        self.builder.load(packs)
+        self._body(self.static, self.step_tokens, build=True)
+
+    def capture_packs(self, packs, warmup_steps: int = 2) -> None:
+        self.builder.load(packs)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(warmup_steps):
+                self._body(self.static, self.step_tokens, build=True)
+        torch.cuda.current_stream().wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self._body(self.static, self.step_tokens, build=True)
+
+    def replay_packs(self, packs) -> None:
+        self.builder.load(packs)
         self.graph.replay()

@@ -46,3 +46,37 @@ def test_graph_replays_match_eager(dev) -> None:
         ne, ng = float(eager.grad_norm), float(graph.grad_norm)
         assert abs(le - lg) <= 1e-3 * abs(le), (i, le, lg)
         assert abs(ne - ng) <= 1e-3 * abs(ne) + 1e-6, (i, ne, ng)
+
+
+def test_graph_replays_with_device_packs_match_eager(dev) -> None:
+    """The same, with each step's packs built on the device inside the step from a
+    token store in HBM (the graph rebuilds them from the table loaded before each
+    replay); the eager twin builds them eagerly from the same tables."""
+    from packbalance_amd.data.device_packs import DeviceTokenStore
+
+    cfg = cfg1_model()
+    rng = np.random.default_rng(1)
+    steps = [W.cfg1_packs(seed=s) for s in range(5)]
+    n_tok = sum(n for st in steps for p in st for n in p)
+    store = DeviceTokenStore(rng.integers(0, cfg.vocab_size, size=n_tok).astype(np.uint32), dev)
+    tables, pos = [], 0
+    for st in steps:
+        packs = []
+        for p in st:
+            packs.append([(pos + sum(p[:i]), n) for i, n in enumerate(p)])
+            pos += sum(p)
+        tables.append(packs)
+    eager = TrainStep(cfg, dev, seq_len=256, store=store)
+    graph = TrainStep(cfg, dev, seq_len=256, store=store)
+    graph.capture_packs(tables[0])
+    for _ in range(2):
+        eager.eager_packs(tables[0])
+    for i in range(1, 5):
+        eager.eager_packs(tables[i])
+        graph.replay_packs(tables[i])
+        torch.cuda.synchronize()
+        le, lg = float(eager.loss_sum), float(graph.loss_sum)
+        ne, ng = float(eager.grad_norm), float(graph.grad_norm)
+        assert abs(le - lg) <= 1e-3 * abs(le), (i, le, lg)
+        assert abs(ne - ng) <= 1e-3 * abs(ne) + 1e-6, (i, ne, ng)
+        assert float(graph.step_tokens) == sum(sum(p) for p in steps[i])
