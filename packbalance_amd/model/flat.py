@@ -78,6 +78,7 @@ class FlatParams:
         self.param.grad = self.grad
         self._shadow: dict[torch.dtype, torch.Tensor] = {}
         self._cache: dict[tuple, torch.Tensor] = {}
+        self._tcache: dict[tuple, tuple[int, torch.Tensor]] = {}
         self._held = False
         self._fresh: set[torch.dtype] = set()  # copies known to equal the master weights
         self.refreshes = 0  # number of compute-copy rewrites (host-side counter)
@@ -116,6 +117,34 @@ class FlatParams:
             return self._group(self.master, params, "master")
         return self._group(self._shadow_buf(dtype), params, dtype)
 
+    def transposed(self, groups, dtype: torch.dtype) -> torch.Tensor:
+        """[len(groups), cols, rows]: each group's compute-dtype weight matrix transposed.
+
+        The groups (one per layer, e.g. every layer's stacked q/k/v) must have one
+        shape and sit at a constant stride in the store, so one strided copy
+        transposes them all.  Rebuilt into the same buffer whenever the compute
+        copy was rewritten.  (hipBLASLt runs the input-gradient products
+        dx = dy W fastest with W given transposed.)"""
+        key = (dtype, tuple(id(g[0]) for g in groups))
+        hit = self._tcache.get(key)
+        if hit is not None and hit[0] == self.refreshes:
+            return hit[1]
+        buf = self.master if dtype == torch.float32 else self._shadow_buf(dtype)
+        first = [self._off[id(g[0])][0] for g in groups]
+        rows = sum(p.shape[0] for p in groups[0])
+        cols = int(groups[0][0].shape[1])
+        stride = first[1] - first[0] if len(groups) > 1 else rows * cols
+        for i, g in enumerate(groups):
+            if first[i] != first[0] + i * stride or sum(p.shape[0] for p in g) != rows:
+                raise ValueError("transposed(): groups must share a shape and a constant stride")
+        src = buf.as_strided((len(groups), rows, cols), (stride, cols, 1), first[0])
+        dst = hit[1] if hit is not None else torch.empty((len(groups), cols, rows), dtype=buf.dtype,
+                                                          device=buf.device)
+        with torch.no_grad():
+            dst.copy_(src.transpose(1, 2))
+        self._tcache[key] = (self.refreshes, dst)
+        return dst
+
     def grad_of(self, params) -> torch.Tensor:
         """The fp32 gradient of ``params`` (adjacent), as one matrix."""
         return self._group(self.grad, params, "grad")
@@ -133,7 +162,11 @@ class FlatParams:
         """Round the master weights to ``dtype`` (no-op for fp32 or inside ``hold``).
 
         Returns True when the copy was rewritten."""
-        if dtype == torch.float32 or self._held:
+        if dtype == torch.float32:
+            if not self._held:
+                self.refreshes += 1  # fp32 "copies" are the masters: derived views go stale
+            return False
+        if self._held:
             return False
         with torch.no_grad():
             self._shadow_buf(dtype).copy_(self.master)

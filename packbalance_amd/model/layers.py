@@ -111,32 +111,40 @@ def _rows(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     return t if t.stride(-1) == 1 else t.contiguous()
 
 
+def _dx_weight(w: torch.Tensor, wt: torch.Tensor | None) -> torch.Tensor:
+    """W for dx = dy W: the transposed copy viewed back (the layout hipBLASLt runs
+    fastest for these shapes) when there is one."""
+    return w if wt is None else wt.t()
+
+
 class _Linear(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, w, g):
+    def forward(ctx, x, w, g, wt):
         x2 = _rows(x, w.dtype)
         y = torch.mm(x2, w.t())
         ctx.save_for_backward(x2, w)
-        ctx.g, ctx.x_dtype, ctx.x_shape = g, x.dtype, x.shape
+        ctx.g, ctx.wt, ctx.x_dtype, ctx.x_shape = g, wt, x.dtype, x.shape
         return y.view(*x.shape[:-1], w.shape[0])
 
     @staticmethod
     def backward(ctx, dy):
         x2, w = ctx.saved_tensors
         dy2 = _rows(dy, w.dtype)
-        dx = _mm(dy2, w, ctx.x_dtype)
+        dx = _mm(dy2, _dx_weight(w, ctx.wt), ctx.x_dtype)
         _accumulate_wgrad(ctx.g, dy2, x2)
-        return dx.view(ctx.x_shape), None, None
+        return dx.view(ctx.x_shape), None, None, None
 
 
-def linear(x: torch.Tensor, w: torch.Tensor, g: torch.Tensor) -> torch.Tensor:
-    """``x @ w.T``; backward returns dx in x's dtype and adds dW into ``g`` (fp32)."""
-    return _Linear.apply(x, w, g)
+def linear(x: torch.Tensor, w: torch.Tensor, g: torch.Tensor,
+           wt: torch.Tensor | None = None) -> torch.Tensor:
+    """``x @ w.T``; backward returns dx in x's dtype and adds dW into ``g`` (fp32).
+    ``wt`` (optional) is ``w`` transposed and contiguous, used for dx."""
+    return _Linear.apply(x, w, g, wt)
 
 
 class _QKVRope(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, w, g, cos, sin, hq, hkv, hd):
+    def forward(ctx, x, w, g, cos, sin, hq, hkv, hd, wt):
         b, s, dm = x.shape
         x2 = _rows(x, w.dtype)
         qkv = torch.mm(x2, w.t())  # [T, (hq + 2 hkv) hd]
@@ -148,7 +156,7 @@ class _QKVRope(torch.autograd.Function):
         kr = torch.empty((b, s, hkv, hd), dtype=qkv.dtype, device=x.device).transpose(1, 2)
         _rope(q, k, qr, kr, cos, sin, 0)
         ctx.save_for_backward(x2, w, cos, sin)
-        ctx.g, ctx.dims, ctx.x_dtype = g, (b, s, dm, hq, hkv, hd), x.dtype
+        ctx.g, ctx.wt, ctx.dims, ctx.x_dtype = g, wt, (b, s, dm, hq, hkv, hd), x.dtype
         return qr, kr, v
 
     @staticmethod
@@ -172,24 +180,24 @@ class _QKVRope(torch.autograd.Function):
             ov.zero_()
         else:
             ov.copy_(dv)
-        dx = _mm(dqkv, w, ctx.x_dtype)
+        dx = _mm(dqkv, _dx_weight(w, ctx.wt), ctx.x_dtype)
         _accumulate_wgrad(ctx.g, dqkv, x2)
-        return dx.view(b, s, dm), None, None, None, None, None, None, None
+        return dx.view(b, s, dm), None, None, None, None, None, None, None, None
 
 
-def qkv_rope(x, w, g, cos, sin, hq: int, hkv: int, hd: int):
+def qkv_rope(x, w, g, cos, sin, hq: int, hkv: int, hd: int, wt: torch.Tensor | None = None):
     """q [B, hq, S, hd] and k [B, hkv, S, hd] (RoPE applied) and v, from one GEMM
     against the stacked [q; k; v] weight ``w``; backward adds dW into ``g``."""
     N.require_device(x, w, op="qkv_rope")
     if x.dim() != 3 or w.shape != ((hq + 2 * hkv) * hd, x.shape[-1]):
         raise ValueError(f"qkv_rope: x {tuple(x.shape)} / w {tuple(w.shape)} do not match "
                          f"hq={hq} hkv={hkv} hd={hd}")
-    return _QKVRope.apply(x, w, g, cos, sin, hq, hkv, hd)
+    return _QKVRope.apply(x, w, g, cos, sin, hq, hkv, hd, wt)
 
 
 class _GateUpSwiGLU(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, w, g):
+    def forward(ctx, x, w, g, wt):
         x2 = _rows(x, w.dtype)
         gu = torch.mm(x2, w.t())  # [T, 2F]: gate | up
         t, f2 = gu.shape
@@ -198,7 +206,7 @@ class _GateUpSwiGLU(torch.autograd.Function):
         N.call("pb_swiglu_fwd_rows", gu.data_ptr(), f2, gu[:, f:].data_ptr(), f2, a.data_ptr(), f,
                t, f, N.dtype_code(gu), N.stream_ptr(gu))
         ctx.save_for_backward(x2, w, gu)
-        ctx.g, ctx.x_dtype, ctx.x_shape = g, x.dtype, x.shape
+        ctx.g, ctx.wt, ctx.x_dtype, ctx.x_shape = g, wt, x.dtype, x.shape
         return a.view(*x.shape[:-1], f)
 
     @staticmethod
@@ -211,17 +219,18 @@ class _GateUpSwiGLU(torch.autograd.Function):
         N.call("pb_swiglu_bwd_rows", gu.data_ptr(), f2, gu[:, f:].data_ptr(), f2, da2.data_ptr(),
                da2.stride(0), dgu.data_ptr(), f2, dgu[:, f:].data_ptr(), f2, t, f,
                N.dtype_code(gu), N.stream_ptr(gu))
-        dx = _mm(dgu, w, ctx.x_dtype)
+        dx = _mm(dgu, _dx_weight(w, ctx.wt), ctx.x_dtype)
         _accumulate_wgrad(ctx.g, dgu, x2)
-        return dx.view(ctx.x_shape), None, None
+        return dx.view(ctx.x_shape), None, None, None
 
 
-def gate_up_swiglu(x: torch.Tensor, w: torch.Tensor, g: torch.Tensor) -> torch.Tensor:
+def gate_up_swiglu(x: torch.Tensor, w: torch.Tensor, g: torch.Tensor,
+                   wt: torch.Tensor | None = None) -> torch.Tensor:
     """``silu(x @ Wg.T) * (x @ Wu.T)`` from one GEMM against ``w`` = [Wg; Wu]."""
     N.require_device(x, w, op="gate_up_swiglu")
     if w.shape[0] % 2 or w.shape[1] != x.shape[-1]:
         raise ValueError(f"gate_up_swiglu: w {tuple(w.shape)} does not match x {tuple(x.shape)}")
-    return _GateUpSwiGLU.apply(x, w, g)
+    return _GateUpSwiGLU.apply(x, w, g, wt)
 
 
 class _Embed(torch.autograd.Function):

@@ -99,11 +99,13 @@ class LlamaMLP(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return self.down_proj(swiglu(self.gate_proj(x), self.up_proj(x)))
 
-    def fused(self, x: torch.Tensor, flat: FlatParams, dt: torch.dtype) -> torch.Tensor:
-        gu = [self.gate_proj.weight, self.up_proj.weight]
-        a = L.gate_up_swiglu(x, flat.weight(gu, dt), flat.grad_of(gu))
-        dn = [self.down_proj.weight]
-        return L.linear(a, flat.weight(dn, dt), flat.grad_of(dn))
+    def groups(self):
+        return {"gu": [self.gate_proj.weight, self.up_proj.weight], "down": [self.down_proj.weight]}
+
+    def fused(self, x: torch.Tensor, flat: FlatParams, dt: torch.dtype, wt: dict) -> torch.Tensor:
+        gr = self.groups()
+        a = L.gate_up_swiglu(x, flat.weight(gr["gu"], dt), flat.grad_of(gr["gu"]), wt["gu"])
+        return L.linear(a, flat.weight(gr["down"], dt), flat.grad_of(gr["down"]), wt["down"])
 
 
 class LlamaAttention(nn.Module):
@@ -125,15 +127,19 @@ class LlamaAttention(nn.Module):
         out = attention_forward(q, k, v, doc_ids, block_mask=block_mask, backend=self.backend)
         return self.o_proj(out.transpose(1, 2).contiguous().view(b, s, -1))
 
-    def fused(self, x, cos, sin, doc_ids, block_mask, flat: FlatParams, dt: torch.dtype):
+    def groups(self):
+        return {"qkv": [self.q_proj.weight, self.k_proj.weight, self.v_proj.weight],
+                "o": [self.o_proj.weight]}
+
+    def fused(self, x, cos, sin, doc_ids, block_mask, flat: FlatParams, dt: torch.dtype,
+              wt: dict):
         b, s, _ = x.shape
-        qkv = [self.q_proj.weight, self.k_proj.weight, self.v_proj.weight]
-        q, k, v = L.qkv_rope(x, flat.weight(qkv, dt), flat.grad_of(qkv), cos, sin,
-                             self.n_heads, self.n_kv_heads, self.head_dim)
+        gr = self.groups()
+        q, k, v = L.qkv_rope(x, flat.weight(gr["qkv"], dt), flat.grad_of(gr["qkv"]), cos, sin,
+                             self.n_heads, self.n_kv_heads, self.head_dim, wt["qkv"])
         out = attention_forward(q, k, v, doc_ids, block_mask=block_mask, backend=self.backend)
         o = out.transpose(1, 2).reshape(b, s, -1)
-        wo = [self.o_proj.weight]
-        return L.linear(o, flat.weight(wo, dt), flat.grad_of(wo))
+        return L.linear(o, flat.weight(gr["o"], dt), flat.grad_of(gr["o"]), wt["o"])
 
 
 class LlamaDecoderLayer(nn.Module):
@@ -149,7 +155,7 @@ class LlamaDecoderLayer(nn.Module):
         return hidden + self.mlp(self.post_attention_layernorm(hidden))
 
     def fused(self, hidden, pending, cos, sin, doc_ids, block_mask, flat: FlatParams,
-              dt: torch.dtype):
+              dt: torch.dtype, wt: dict):
         """(new residual, MLP output still to be added): the previous layer's MLP
         output ``pending`` is added inside this layer's first norm."""
         eps = self.input_layernorm.eps
@@ -158,9 +164,9 @@ class LlamaDecoderLayer(nn.Module):
             x = rmsnorm_to(hidden, w1, eps, dt, dw_acc=flat.grad_of([w1]))
         else:
             hidden, x = add_rmsnorm(hidden, pending, w1, eps, dt, dw_acc=flat.grad_of([w1]))
-        a = self.self_attn.fused(x, cos, sin, doc_ids, block_mask, flat, dt)
+        a = self.self_attn.fused(x, cos, sin, doc_ids, block_mask, flat, dt, wt)
         hidden, x = add_rmsnorm(hidden, a, w2, eps, dt, dw_acc=flat.grad_of([w2]))
-        return hidden, self.mlp.fused(x, flat, dt)
+        return hidden, self.mlp.fused(x, flat, dt, wt)
 
 
 class LlamaForCausalLM(nn.Module):
@@ -215,9 +221,16 @@ class LlamaForCausalLM(nn.Module):
             cos, sin = self.rotary(position_ids)
             if block_mask is None:
                 block_mask = build_doc_block_mask(doc_ids, self.cfg.n_heads)
-            pending = None
+            # Every layer's projection weights transposed, one copy per kind (dx GEMMs).
+            kinds = {}
             for layer in self.layers:
-                hidden, pending = layer.fused(hidden, pending, cos, sin, doc_ids, block_mask, flat, dt)
+                for k, g in {**layer.self_attn.groups(), **layer.mlp.groups()}.items():
+                    kinds.setdefault(k, []).append(g)
+            wts = {k: flat.transposed(g, dt) for k, g in kinds.items()}
+            pending = None
+            for i, layer in enumerate(self.layers):
+                hidden, pending = layer.fused(hidden, pending, cos, sin, doc_ids, block_mask, flat,
+                                              dt, {k: w[i] for k, w in wts.items()})
             _, y = add_rmsnorm(hidden, pending, self.norm.weight, self.norm.eps, dt,
                                dw_acc=flat.grad_of([self.norm.weight]))
             kw = dict(ignore_index=-100, z_loss_coeff=self.cfg.z_loss_coeff)

@@ -54,7 +54,7 @@ def test_qkv_rope_matches_fp32(b, s, dm, hq, hkv, hd, dev) -> None:
     pos = torch.randint(0, s, (b, s), generator=g).to(dev)
     cos, sin = RotaryEmbedding(hd, s).to(dev)(pos)
     xr = x.clone().requires_grad_(True)
-    q, k, v = L.qkv_rope(xr, w, acc, cos, sin, hq, hkv, hd)
+    q, k, v = L.qkv_rope(xr, w, acc, cos, sin, hq, hkv, hd, w.t().contiguous())
     assert q.shape == (b, hq, s, hd) and k.shape == (b, hkv, s, hd) and v.shape == (b, hkv, s, hd)
     gq, gk, gv = (torch.randn(t.shape, generator=g).to(dev, BF) for t in (q, k, v))
     torch.autograd.backward((q, k, v), (gq, gk, gv))
@@ -78,8 +78,10 @@ def test_qkv_rope_matches_fp32(b, s, dm, hq, hkv, hd, dev) -> None:
     assert _rel(acc - acc0, 2 * wf.grad) < 1e-2
 
 
-@pytest.mark.parametrize("t,dm,f", [(2048, 768, 2048), (256, 128, 344)])
-def test_gate_up_swiglu_and_down_proj_match_fp32(t, dm, f, dev) -> None:
+@pytest.mark.parametrize("t,dm,f,use_wt", [(2048, 768, 2048, True), (2048, 768, 2048, False),
+                                            (256, 128, 344, True)])
+def test_gate_up_swiglu_and_down_proj_match_fp32(t, dm, f, use_wt, dev) -> None:
+    """use_wt: dx computed from transposed weight copies, as the model does."""
     g = torch.Generator().manual_seed(1)
     x = torch.randn(1, t, dm, generator=g).to(dev, BF)
     wgu = (torch.randn(2 * f, dm, generator=g) * 0.05).to(dev, BF)
@@ -88,8 +90,10 @@ def test_gate_up_swiglu_and_down_proj_match_fp32(t, dm, f, dev) -> None:
     ad0 = torch.randn(dm, f, generator=g).to(dev)
     agu, ad = agu0.clone(), ad0.clone()
     xr = x.clone().requires_grad_(True)
-    a = L.gate_up_swiglu(xr, wgu, agu)
-    y = L.linear(a, wd, ad)
+    wgu_t = wgu.t().contiguous() if use_wt else None
+    wd_t = wd.t().contiguous() if use_wt else None
+    a = L.gate_up_swiglu(xr, wgu, agu, wgu_t)
+    y = L.linear(a, wd, ad, wd_t)
     assert a.dtype == BF and y.dtype == BF and y.shape == (1, t, dm)
     gy = torch.randn(y.shape, generator=g).to(dev, BF)
     y.backward(gy)
