@@ -106,7 +106,7 @@ def make_flush(dev):
 
 
 # ---------------------------------------------------------------- cfg2 train step
-def train_step_bench(steps: int, warmup: int, dev, use_graph: bool = True):
+def train_step_bench(steps: int, warmup: int, dev, use_graph: bool = True, streams: int = 4):
     import numpy as np
     import torch
 
@@ -131,7 +131,9 @@ def train_step_bench(steps: int, warmup: int, dev, use_graph: bool = True):
             packs.append([(pos + sum(p[:i]), n) for i, n in enumerate(p)])
             pos += sum(p)
         step_packs.append(packs)
-    ts = TrainStep(cfg, dev, store=store)
+    # The step's micro-batches run concurrently on `streams` streams (one fp32
+    # gradient slot each, summed by the optimizer's norm pass).
+    ts = TrainStep(cfg, dev, store=store, streams=streams)
     model = ts.model
     if use_graph:
         ts.capture_packs(step_packs[0])
@@ -158,6 +160,7 @@ def train_step_bench(steps: int, warmup: int, dev, use_graph: bool = True):
         "model_tflops": flops / dt / 1e12,
         "hip_graph": use_graph,
         "packs_built_on_device": True,
+        "micro_batch_streams": len(ts.streams) or 1,
     }
     # The first pack of the first timed step, on the host, for the CPU baseline.
     first = build_pack_batch(store, [step_packs[warmup][0]], 2048)
@@ -412,6 +415,8 @@ def main() -> int:
     ap.add_argument("--skip-kernels", action="store_true")
     ap.add_argument("--eager", action="store_true",
                     help="run the training step eagerly instead of as one captured HIP graph")
+    ap.add_argument("--streams", type=int, default=4,
+                    help="streams the step's micro-batches run on concurrently (1: one after another)")
     ap.add_argument("--only", choices=["train", "attention", "lmhead_ce", "ce_rows", "norm_act",
                                        "copy"],
                     default=None, help="run one part only (for profiling)")
@@ -445,7 +450,8 @@ def main() -> int:
 
     log(f"train step: {args.warmup} warmup + {args.steps} timed steps")
     train, model, cfg, cpu_pack = train_step_bench(args.steps, args.warmup, dev,
-                                                   use_graph=not args.eager)
+                                                   use_graph=not args.eager,
+                                                   streams=args.streams)
     log(f"train: {train['tok_s']:.0f} tok/s, {train['ms_per_step']:.2f} ms/step")
     if args.only == "train":
         print(json.dumps({"train": train}), flush=True)
@@ -496,6 +502,7 @@ def main() -> int:
             "params": train["params"],
             "model_tflops": train["model_tflops"],
             "hip_graph": train["hip_graph"],
+            "micro_batch_streams": train["micro_batch_streams"],
         },
         "masked_attn_tflops": kernels.get("attention", {}).get("fwd_bwd_tflops"),
         "ce_gbps": kernels.get("ce_rows", {}).get("gbps"),

@@ -278,20 +278,24 @@ int pb_pack_tensors(const void *store, int store_elem_bytes, int64_t store_len,
  * (packbalance/train/train.py:58-69,353-362; profiling/bench_train.py:79-85,
  * 115-116), for uniform hyper-parameters over parameters stored as one flat
  * buffer:
+ *   grad = sum of grad_slots buffers grad_slot_stride elements apart (one
+ *   per concurrently run micro-batch, say); with more than one slot the sum
+ *   is written back into slot 0 (grad[0..n));
  *   norm = ||grad||_2 -> *grad_norm_out (may be NULL);
  *   c = min(max_grad_norm / (norm + 1e-6), 1)  (1 when max_grad_norm <= 0);
  *   *step += 1 (device fp32, the optimizer's step count);
  *   p -= lr*wd*p;  m = b1 m + (1-b1) c g;  v = b2 v + (1-b2) (c g)^2;
  *   p -= lr/(1-b1^t) * m / (sqrt(v)/sqrt(1-b2^t) + eps);
  *   param_copy (may be NULL) = p rounded to copy_dtype.
- * grad is read, never written (the clipped gradient is not stored back).
+ * The clipped gradient is not stored back.
  * Buffers 16-byte aligned (param_copy 8-byte); workspace:
  * pb_clip_adamw_workspace_bytes(n) bytes, 16-byte aligned.                  */
 int64_t pb_clip_adamw_workspace_bytes(int64_t n);
-int pb_clip_adamw_step(float *param, const float *grad, float *exp_avg, float *exp_avg_sq,
-                       void *param_copy, int copy_dtype, int64_t n, float lr, float beta1,
-                       float beta2, float eps, float weight_decay, float max_grad_norm,
-                       float *step, float *grad_norm_out, void *workspace, void *stream);
+int pb_clip_adamw_step(float *param, float *grad, int grad_slots, int64_t grad_slot_stride,
+                       float *exp_avg, float *exp_avg_sq, void *param_copy, int copy_dtype,
+                       int64_t n, float lr, float beta1, float beta2, float eps,
+                       float weight_decay, float max_grad_norm, float *step,
+                       float *grad_norm_out, void *workspace, void *stream);
 
 /* ---- Rotary position embedding (q and k in one launch) ------------------
  * Replaces packbalance/model/rope.py:34-42 (apply_rotary_pos_emb, NeoX

@@ -111,7 +111,8 @@ SIGNATURES: dict[str, tuple] = {
     "pb_clip_adamw_workspace_bytes": (_i64, [_i64]),
     "pb_clip_adamw_step": (
         _i32,
-        [_p, _p, _p, _p, _p, _i32, _i64, _f32, _f32, _f32, _f32, _f32, _f32, _p, _p, _p, _p],
+        [_p, _p, _i32, _i64, _p, _p, _p, _i32, _i64, _f32, _f32, _f32, _f32, _f32, _f32, _p, _p, _p,
+         _p],
     ),
     "pb_rope_qk": (
         _i32,

@@ -17,8 +17,13 @@
 // and, optionally, the updated p rounded into a bf16/fp16 copy (the weights
 // the next step's matmuls read), so no separate cast pass runs.
 //
+// The gradient may arrive in several slots (grad_slots buffers slot_stride
+// elements apart, e.g. one per concurrently run micro-batch): it is their sum,
+// which the first pass forms and writes back into slot 0.
+//
 // Three launches, all streaming with 16-byte non-temporal accesses:
-//   1. sq_partial: per-workgroup sums of g^2 (fixed grid, fixed order);
+//   1. sq_partial: sums the slots (when more than one) into slot 0, and
+//                  per-workgroup sums of g^2 (fixed grid, fixed order);
 //   2. prepare:    one workgroup folds the partials in fp64, writes the norm,
 //                  advances the device-resident step and stores the per-step
 //                  scalars (clip factor, step size, sqrt(1 - b2^t));
@@ -47,28 +52,46 @@ struct Scalars {
   float pad;
 };
 
-__global__ __launch_bounds__(kThreads) void sq_partial(const float *__restrict__ g, int64_t n,
+// Squared norm of the slot sum, which is written back into slot 0 when there
+// are several slots (slot order fixed, so the sum is deterministic).
+__global__ __launch_bounds__(kThreads) void sq_partial(float *__restrict__ g, int64_t n, int slots,
+                                                       int64_t slot_stride,
                                                        float *__restrict__ partial) {
   __shared__ float red[kThreads / 64];
   const int64_t nvec = n / 4;
   const int64_t stride = (int64_t)gridDim.x * kThreads;
-  float s0 = 0.f, s1 = 0.f;
-  int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  for (; i + stride < nvec; i += 2 * stride) {
-    const f32x4 a = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(g) + i);
-    const f32x4 b = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(g) + i + stride);
-    s0 += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
-    s1 += b.x * b.x + b.y * b.y + b.z * b.z + b.w * b.w;
-  }
-  if (i < nvec) {
-    const f32x4 a = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(g) + i);
-    s0 += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+  float s0 = 0.f;
+  if (slots == 1) {
+    float s1 = 0.f;
+    int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    for (; i + stride < nvec; i += 2 * stride) {
+      const f32x4 a = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(g) + i);
+      const f32x4 b = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(g) + i + stride);
+      s0 += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+      s1 += b.x * b.x + b.y * b.y + b.z * b.z + b.w * b.w;
+    }
+    if (i < nvec) {
+      const f32x4 a = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(g) + i);
+      s0 += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+    }
+    s0 += s1;
+  } else {
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < nvec; i += stride) {
+      f32x4 a = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(g) + i);
+      for (int sl = 1; sl < slots; ++sl)
+        a += __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(g + sl * slot_stride) + i);
+      reinterpret_cast<f32x4 *>(g)[i] = a;
+      s0 += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+    }
   }
   if (blockIdx.x == 0 && threadIdx.x < n - nvec * 4) {
-    const float t = g[nvec * 4 + threadIdx.x];
-    s1 += t * t;
+    const int64_t j = nvec * 4 + threadIdx.x;
+    float t = g[j];
+    for (int sl = 1; sl < slots; ++sl) t += g[sl * slot_stride + j];
+    if (slots > 1) g[j] = t;
+    s0 += t * t;
   }
-  float s = wave_sum(s0 + s1);
+  float s = wave_sum(s0);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -208,11 +231,12 @@ extern "C" int64_t pb_clip_adamw_workspace_bytes(int64_t n) {
   return (int64_t)(pb::kNormWgs * sizeof(float) + 256);
 }
 
-extern "C" int pb_clip_adamw_step(float *param, const float *grad, float *exp_avg,
-                                  float *exp_avg_sq, void *param_copy, int copy_dtype, int64_t n,
-                                  float lr, float beta1, float beta2, float eps,
-                                  float weight_decay, float max_grad_norm, float *step,
-                                  float *grad_norm_out, void *workspace, void *stream) {
+extern "C" int pb_clip_adamw_step(float *param, float *grad, int grad_slots,
+                                  int64_t grad_slot_stride, float *exp_avg, float *exp_avg_sq,
+                                  void *param_copy, int copy_dtype, int64_t n, float lr,
+                                  float beta1, float beta2, float eps, float weight_decay,
+                                  float max_grad_norm, float *step, float *grad_norm_out,
+                                  void *workspace, void *stream) {
   using namespace pb;
   clear_error();
   PB_CHECK_ARG(param && grad && exp_avg && exp_avg_sq && step && workspace,
@@ -225,12 +249,16 @@ extern "C" int pb_clip_adamw_step(float *param, const float *grad, float *exp_av
                "pb_clip_adamw_step: buffers must be 16-byte aligned (the copy 8-byte aligned)");
   PB_CHECK_ARG(beta1 >= 0.f && beta1 < 1.f && beta2 >= 0.f && beta2 < 1.f && eps > 0.f,
                "pb_clip_adamw_step: bad hyper-parameters");
+  PB_CHECK_ARG(grad_slots >= 1 && grad_slots <= 64 &&
+                   (grad_slots == 1 || (grad_slot_stride >= n && grad_slot_stride % 4 == 0)),
+               "pb_clip_adamw_step: bad gradient slots (count 1..64, stride >= n, %% 4 == 0)");
   // Keeps the update grid (n / 4 / 512 workgroups) below 2^31.
   PB_CHECK_SUPPORTED(n < (1LL << 38), "pb_clip_adamw_step: too large");
   hipStream_t st = as_stream(stream);
   float *partial = static_cast<float *>(workspace);
   Scalars *sc = reinterpret_cast<Scalars *>(static_cast<char *>(workspace) + kNormWgs * sizeof(float));
-  hipLaunchKernelGGL(sq_partial, dim3(kNormWgs), dim3(kThreads), 0, st, grad, n, partial);
+  hipLaunchKernelGGL(sq_partial, dim3(kNormWgs), dim3(kThreads), 0, st, grad, n, grad_slots,
+                     grad_slot_stride, partial);
   hipLaunchKernelGGL(prepare, dim3(1), dim3(kThreads), 0, st, partial, kNormWgs, max_grad_norm, lr,
                      beta1, beta2, step, grad_norm_out, sc);
   int rc = launch_status("pb_clip_adamw_step(norm)");

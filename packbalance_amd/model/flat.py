@@ -13,6 +13,13 @@ Every ``nn.Parameter`` of the model becomes a view into the master buffer
 * matmul backward passes accumulate weight gradients in fp32 straight into
   the gradient buffer (no bf16 dW, no cast, no separate add per micro-batch).
 
+Micro-batches run concurrently (one stream each) must not add into one
+gradient buffer at once, so the store can hold several gradient SLOTS: rows
+of one ``[slots, n]`` buffer, slot 0 being ``grad`` (what every ``p.grad``
+views).  Inside ``accumulate_into(i)`` the weight-gradient targets handed out
+by ``grad_of`` are slot ``i``'s; the fused optimizer step sums the slots into
+slot 0 before clipping.
+
 The compute-dtype copy is what torch's autocast computes on the fly (each
 fp32 weight rounded to bf16 once per autocast region); here it is one cast
 kernel over the whole buffer, run by ``refresh`` -- by the model on every
@@ -35,7 +42,10 @@ def _align(n: int) -> int:
 
 
 class FlatParams:
-    def __init__(self, model: nn.Module, groups: list[list[nn.Parameter]] = ()) -> None:
+    def __init__(self, model: nn.Module, groups: list[list[nn.Parameter]] = (),
+                 grad_slots: int = 1) -> None:
+        if grad_slots < 1:
+            raise ValueError(f"grad_slots must be >= 1, got {grad_slots}")
         named = list(model.named_parameters())
         if not named:
             raise ValueError("model has no parameters")
@@ -62,7 +72,9 @@ class FlatParams:
         total = _align(off)
         self.device = dev
         self.master = torch.zeros(total, dtype=torch.float32, device=dev)
-        self.grad = torch.zeros(total, dtype=torch.float32, device=dev)
+        self._grads = torch.zeros((grad_slots, total), dtype=torch.float32, device=dev)
+        self.grad = self._grads[0]
+        self._slot = 0
         self._params = [p for _, p in named]
         with torch.no_grad():
             for p in self._params:
@@ -146,8 +158,29 @@ class FlatParams:
         return dst
 
     def grad_of(self, params) -> torch.Tensor:
-        """The fp32 gradient of ``params`` (adjacent), as one matrix."""
-        return self._group(self.grad, params, "grad")
+        """The fp32 gradient of ``params`` (adjacent), as one matrix, in the active slot."""
+        return self._group(self._grads[self._slot], params, ("grad", self._slot))
+
+    @property
+    def grad_slots(self) -> int:
+        return self._grads.shape[0]
+
+    @property
+    def grad_slot_stride(self) -> int:
+        """Elements from one gradient slot to the next."""
+        return self._grads.stride(0)
+
+    @contextlib.contextmanager
+    def accumulate_into(self, slot: int):
+        """Weight gradients of the forwards run inside the block go to ``slot``
+        (their backward passes keep that target whenever they run)."""
+        if not 0 <= slot < self.grad_slots:
+            raise ValueError(f"gradient slot {slot} out of range [0, {self.grad_slots})")
+        prev, self._slot = self._slot, slot
+        try:
+            yield
+        finally:
+            self._slot = prev
 
     # ------------------------------------------------------------ compute copy
     def _shadow_buf(self, dtype: torch.dtype) -> torch.Tensor:
@@ -214,4 +247,5 @@ class FlatParams:
                 self.param.grad = self.grad
 
     def zero_grad(self) -> None:
-        self.grad.zero_()
+        """Zero every gradient slot (one fill)."""
+        self._grads.zero_()

@@ -33,9 +33,13 @@ join that an autograd final callback queues at the end of the backward pass;
 the callback runs on the stream that called ``backward()``, which then waits
 for the side stream -- so gradients are complete when ``backward()`` returns,
 eagerly or inside a captured HIP graph (where the wait becomes a graph edge).
+A caller that already runs micro-batches concurrently on several streams has
+the overlap without it and turns it off (``wgrad_on_caller_stream``).
 """
 
 from __future__ import annotations
+
+import contextlib
 
 import torch
 import torch.nn.functional as F
@@ -45,6 +49,18 @@ from packbalance_amd.model.rope import _rope
 
 
 WGRAD_SIDE_STREAM = True
+
+
+@contextlib.contextmanager
+def wgrad_on_caller_stream():
+    """Run weight-gradient GEMMs of the backward passes inside the block on the
+    stream that runs the rest of the pass."""
+    global WGRAD_SIDE_STREAM
+    prev, WGRAD_SIDE_STREAM = WGRAD_SIDE_STREAM, False
+    try:
+        yield
+    finally:
+        WGRAD_SIDE_STREAM = prev
 
 
 class _SideStream:

@@ -188,16 +188,18 @@ class LlamaForCausalLM(nn.Module):
         self._lm_bf16 = None  # (compute copy, its refresh count, wb, wt) of the tied LM head
 
     # ------------------------------------------------------------ flat storage
-    def flat_parameters(self) -> FlatParams:
+    def flat_parameters(self, grad_slots: int = 1) -> FlatParams:
         """The flat store of this model's parameters (created on first use, and again
-        if the parameters were moved or replaced since)."""
-        if self._flat is None or not self._flat.owns(self):
+        if the parameters were moved or replaced since, or more gradient slots are
+        asked for than it has)."""
+        if (self._flat is None or not self._flat.owns(self)
+                or self._flat.grad_slots < grad_slots):
             groups = []
             for layer in self.layers:
                 a, m = layer.self_attn, layer.mlp
                 groups.append([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight])
                 groups.append([m.gate_proj.weight, m.up_proj.weight])
-            self._flat = FlatParams(self, groups)
+            self._flat = FlatParams(self, groups, grad_slots)
             self._lm_bf16 = None
         return self._flat
 
@@ -208,6 +210,27 @@ class LlamaForCausalLM(nn.Module):
         if c is None or c[0] is not w or c[1] != flat.refreshes:
             self._lm_bf16 = c = (w, flat.refreshes) + lmhead_weight_bf16(w)
         return c[2], c[3]
+
+    def _transposed_weights(self, flat: FlatParams, dt: torch.dtype) -> dict:
+        """Every layer's projection weights transposed, one copy per kind (the
+        input-gradient GEMMs read them)."""
+        kinds = {}
+        for layer in self.layers:
+            for k, g in {**layer.self_attn.groups(), **layer.mlp.groups()}.items():
+                kinds.setdefault(k, []).append(g)
+        return {k: flat.transposed(g, dt) for k, g in kinds.items()}
+
+    def prepare(self, dt: torch.dtype) -> None:
+        """Build the weight copies that forwards share (compute copy, transposed
+        weights, LM-head rows) on the current stream.  Forwards run concurrently
+        on other streams after it only read them (their stream waits for this
+        one first); inside ``FlatParams.hold`` they are not rebuilt."""
+        flat = self.flat_parameters()
+        flat.refresh(dt)
+        if dt != torch.float32:
+            self._transposed_weights(flat, dt)
+            if self.cfg.d_model % 8 == 0:
+                self._lm_head(flat, dt)
 
     def forward(self, input_ids, labels, position_ids, doc_ids, block_mask=None):
         dev = input_ids.device
@@ -221,12 +244,7 @@ class LlamaForCausalLM(nn.Module):
             cos, sin = self.rotary(position_ids)
             if block_mask is None:
                 block_mask = build_doc_block_mask(doc_ids, self.cfg.n_heads)
-            # Every layer's projection weights transposed, one copy per kind (dx GEMMs).
-            kinds = {}
-            for layer in self.layers:
-                for k, g in {**layer.self_attn.groups(), **layer.mlp.groups()}.items():
-                    kinds.setdefault(k, []).append(g)
-            wts = {k: flat.transposed(g, dt) for k, g in kinds.items()}
+            wts = self._transposed_weights(flat, dt)
             pending = None
             for i, layer in enumerate(self.layers):
                 hidden, pending = layer.fused(hidden, pending, cos, sin, doc_ids, block_mask, flat,

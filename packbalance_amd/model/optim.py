@@ -9,8 +9,11 @@ so over the flat store they are three launches of ``pb_clip_adamw_step``
 (gradient norm partials, a one-workgroup fold that also advances the
 device-resident step count, the element-wise update), and the update writes
 the bf16 copy the next step's matmuls read.  The step count, the norm and the
-per-step scalars stay on the device (graph-capture safe).  Unlike
-``clip_grad_norm_``, the clipped gradient is not written back into ``.grad``.
+per-step scalars stay on the device (graph-capture safe).  When the store
+holds several gradient slots (micro-batches run concurrently), the norm pass
+first sums them into slot 0, so ``.grad`` ends the step holding the whole
+step's gradient.  Unlike ``clip_grad_norm_``, the clipped gradient is not
+written back into ``.grad``.
 """
 
 from __future__ import annotations
@@ -46,8 +49,8 @@ class FlatAdamW:
         copy = None
         if self.copy_dtype is not None:
             copy = f._shadow_buf(self.copy_dtype)
-        N.call("pb_clip_adamw_step", f.master.data_ptr(), f.grad.data_ptr(),
-               self.exp_avg.data_ptr(), self.exp_avg_sq.data_ptr(),
+        N.call("pb_clip_adamw_step", f.master.data_ptr(), f.grad.data_ptr(), f.grad_slots,
+               f.grad_slot_stride, self.exp_avg.data_ptr(), self.exp_avg_sq.data_ptr(),
                copy.data_ptr() if copy is not None else None,
                N.dtype_code(copy) if copy is not None else N.PB_F32, f.master.numel(),
                self.lr, self.betas[0], self.betas[1], self.eps, self.weight_decay,

@@ -19,6 +19,14 @@ step -- the part of the reference's timed step that loads and copies the
 micro-batches (``bench_train.py:103-111``) -- and the step's token count
 comes from the same table, so a replay needs only the table's copy.
 
+With ``streams > 1`` the micro-batches run concurrently, micro-batch i on
+stream i % streams: at 2048 tokens a micro-batch's kernels fill only part of
+the GPU, so the chains overlap.  Each stream adds its weight gradients into
+its own gradient slot of the flat store (no two streams write one buffer),
+the shared weight copies are built on the step's stream before the fork, and
+the optimizer's norm pass sums the slots -- the same gradient as the
+sequential step up to the order of fp32 additions.
+
 ``capture`` records that whole sequence once into a HIP graph on static
 device buffers (every hot-path op is capture-safe: no host synchronisation,
 device-resident grad scale, all workspaces from the caching allocator);
@@ -33,6 +41,7 @@ from __future__ import annotations
 import torch
 
 from packbalance_amd.data.device_packs import DeviceTokenStore, PackBuilder
+from packbalance_amd.model import layers as L
 from packbalance_amd.model.attention import build_doc_block_mask
 from packbalance_amd.model.llama import LlamaForCausalLM
 from packbalance_amd.model.optim import FlatAdamW
@@ -40,13 +49,17 @@ from packbalance_amd.model.optim import FlatAdamW
 
 class TrainStep:
     def __init__(self, cfg, dev, packs_per_step: int = 4, seq_len: int | None = None,
-                 seed: int = 0, lr: float = 3e-4, store: DeviceTokenStore | None = None):
+                 seed: int = 0, lr: float = 3e-4, store: DeviceTokenStore | None = None,
+                 streams: int = 1):
         self.cfg, self.dev = cfg, dev
         seq_len = seq_len or cfg.max_seq_len
+        streams = max(1, min(int(streams), packs_per_step))
         torch.manual_seed(seed)
         self.model = LlamaForCausalLM(cfg).to(dev)
         self.model.train()
-        self.flat = self.model.flat_parameters()
+        self.flat = self.model.flat_parameters(grad_slots=streams)
+        self.streams = [torch.cuda.Stream(dev) for _ in range(streams)] if streams > 1 else []
+        self.stream_loss = torch.zeros(streams, dtype=torch.float32, device=dev)
         self.opt = FlatAdamW(self.flat, lr=lr, betas=(0.9, 0.95), weight_decay=0.1,
                              max_grad_norm=1.0, copy_dtype=torch.bfloat16)
 
@@ -74,13 +87,35 @@ class TrainStep:
         self.flat.attach_grads()
         self.flat.zero_grad()
         with torch.autocast("cuda", dtype=torch.bfloat16), self.flat.hold(torch.bfloat16):
-            for b in batches:
-                bm = build_doc_block_mask(b["doc_ids"], self.cfg.n_heads)
-                loss = self.model(b["input_ids"], b["labels"], b["position_ids"], b["doc_ids"],
-                                  block_mask=bm)
-                (loss / step_tokens).backward()
-                self.loss_sum += loss.detach()
+            if self.streams:
+                self._concurrent(batches, step_tokens)
+            else:
+                for b in batches:
+                    self._micro_batch(b, step_tokens, self.loss_sum)
         self.grad_norm.copy_(self.opt.step())
+
+    def _micro_batch(self, b, step_tokens, loss_acc) -> None:
+        bm = build_doc_block_mask(b["doc_ids"], self.cfg.n_heads)
+        loss = self.model(b["input_ids"], b["labels"], b["position_ids"], b["doc_ids"],
+                          block_mask=bm)
+        (loss / step_tokens).backward()
+        loss_acc += loss.detach()
+
+    def _concurrent(self, batches, step_tokens) -> None:
+        """Micro-batch i on stream i % k, weight gradients into slot i % k."""
+        main = torch.cuda.current_stream(self.dev)
+        self.model.prepare(torch.bfloat16)
+        self.stream_loss.zero_()
+        for s in self.streams:
+            s.wait_stream(main)
+        with L.wgrad_on_caller_stream():
+            for i, b in enumerate(batches):
+                j = i % len(self.streams)
+                with torch.cuda.stream(self.streams[j]), self.flat.accumulate_into(j):
+                    self._micro_batch(b, step_tokens, self.stream_loss[j])
+        for s in self.streams:
+            main.wait_stream(s)
+        self.loss_sum.copy_(self.stream_loss.sum())
 
     @staticmethod
     def _as_dicts(batch_list):

@@ -85,6 +85,42 @@ def test_flat_adamw_matches_torch_fused_adamw(dev) -> None:
         torch.testing.assert_close(flat.master, ref.detach(), rtol=0, atol=4e-8)
 
 
+def test_flat_adamw_sums_gradient_slots(dev) -> None:
+    """Three gradient slots: the step uses their sum (slot order 0, 1, 2 in fp32),
+    leaves it in slot 0 bit for bit, and otherwise matches the oracle on that sum."""
+    g = torch.Generator().manual_seed(5)
+    mod = torch.nn.Module()
+    mod.register_parameter("a", torch.nn.Parameter(torch.randn(300007, generator=g) * 0.02))
+    mod.register_parameter("b", torch.nn.Parameter(torch.randn(77, generator=g) * 0.02))
+    flat = FlatParams(mod.to(dev), grad_slots=3)
+    assert flat.grad_slots == 3 and flat.grad_slot_stride >= flat.master.numel()
+    n = flat.master.numel()
+    opt = FlatAdamW(flat, max_grad_norm=1.0, copy_dtype=torch.bfloat16, **HP)
+    p = flat.master.double().cpu().numpy().copy()
+    m, v = np.zeros(n), np.zeros(n)
+    step = 0
+    rng = np.random.default_rng(6)
+    for k in range(2):
+        parts = [(rng.standard_normal(n) * 0.01).astype(np.float32) for _ in range(3)]
+        for s, part in enumerate(parts):
+            flat._grads[s].copy_(torch.from_numpy(part))
+        total = (parts[0] + parts[1]) + parts[2]  # fp32, in slot order
+        norm = opt.step()
+        step, onorm = OO.clip_adamw_step(p, total.astype(np.float64), m, v, step, max_norm=1.0,
+                                         **HP)
+        torch.cuda.synchronize()
+        assert np.array_equal(flat.grad.cpu().numpy(), total)
+        assert abs(float(norm) - onorm) <= 2e-6 * onorm
+        ulp = float(np.spacing(np.float32(np.abs(p).max())))
+        assert np.abs(flat.master.double().cpu().numpy() - p).max() <= (k + 1) * ulp + 1e-5 * HP["lr"]
+    with flat.accumulate_into(2):
+        assert flat.grad_of([mod.b]).data_ptr() == flat._grads[2].data_ptr() + \
+            (mod.b.data_ptr() - flat.master.data_ptr())
+    with pytest.raises(ValueError):
+        with flat.accumulate_into(3):
+            pass
+
+
 def test_flat_adamw_rejects_bad_hyperparameters(dev) -> None:
     flat = _store([64], dev)
     with pytest.raises(ValueError):
