@@ -106,7 +106,8 @@ def make_flush(dev):
 
 
 # ---------------------------------------------------------------- cfg2 train step
-def train_step_bench(steps: int, warmup: int, dev, use_graph: bool = True, streams: int = 4):
+def train_step_bench(steps: int, warmup: int, dev, use_graph: bool = True, streams: int = 2,
+                     packs_per_micro_batch: int = 2):
     import numpy as np
     import torch
 
@@ -131,9 +132,12 @@ def train_step_bench(steps: int, warmup: int, dev, use_graph: bool = True, strea
             packs.append([(pos + sum(p[:i]), n) for i, n in enumerate(p)])
             pos += sum(p)
         step_packs.append(packs)
-    # The step's micro-batches run concurrently on `streams` streams (one fp32
-    # gradient slot each, summed by the optimizer's norm pass).
-    ts = TrainStep(cfg, dev, store=store, streams=streams)
+    # The step's 4 packs run as micro-batches of `packs_per_micro_batch` packs
+    # ([k, 2048] each; the step's gradient is the same sum over packs), and the
+    # micro-batches run concurrently on `streams` streams (one fp32 gradient
+    # slot each, summed by the optimizer's norm pass).
+    ts = TrainStep(cfg, dev, store=store, streams=streams,
+                   packs_per_micro_batch=packs_per_micro_batch)
     model = ts.model
     if use_graph:
         ts.capture_packs(step_packs[0])
@@ -161,6 +165,7 @@ def train_step_bench(steps: int, warmup: int, dev, use_graph: bool = True, strea
         "hip_graph": use_graph,
         "packs_built_on_device": True,
         "micro_batch_streams": len(ts.streams) or 1,
+        "packs_per_micro_batch": ts.k,
     }
     # The first pack of the first timed step, on the host, for the CPU baseline.
     first = build_pack_batch(store, [step_packs[warmup][0]], 2048)
@@ -415,7 +420,9 @@ def main() -> int:
     ap.add_argument("--skip-kernels", action="store_true")
     ap.add_argument("--eager", action="store_true",
                     help="run the training step eagerly instead of as one captured HIP graph")
-    ap.add_argument("--streams", type=int, default=4,
+    ap.add_argument("--packs-per-micro-batch", type=int, default=2,
+                    help="packs run as one [k, 2048] micro-batch (1, 2 or 4)")
+    ap.add_argument("--streams", type=int, default=2,
                     help="streams the step's micro-batches run on concurrently (1: one after another)")
     ap.add_argument("--only", choices=["train", "attention", "lmhead_ce", "ce_rows", "norm_act",
                                        "copy"],
@@ -451,7 +458,8 @@ def main() -> int:
     log(f"train step: {args.warmup} warmup + {args.steps} timed steps")
     train, model, cfg, cpu_pack = train_step_bench(args.steps, args.warmup, dev,
                                                    use_graph=not args.eager,
-                                                   streams=args.streams)
+                                                   streams=args.streams,
+                                                   packs_per_micro_batch=args.packs_per_micro_batch)
     log(f"train: {train['tok_s']:.0f} tok/s, {train['ms_per_step']:.2f} ms/step")
     if args.only == "train":
         print(json.dumps({"train": train}), flush=True)
@@ -503,6 +511,7 @@ def main() -> int:
             "model_tflops": train["model_tflops"],
             "hip_graph": train["hip_graph"],
             "micro_batch_streams": train["micro_batch_streams"],
+            "packs_per_micro_batch": train["packs_per_micro_batch"],
         },
         "masked_attn_tflops": kernels.get("attention", {}).get("fwd_bwd_tflops"),
         "ce_gbps": kernels.get("ce_rows", {}).get("gbps"),

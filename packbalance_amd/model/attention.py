@@ -13,6 +13,10 @@ Drop-in for the reference ``packbalance/model/attention.py``:
   compile_attention=True)`` (attention.py:98-125) runs the hand-written MFMA
   kernels for ``backend`` "auto" / "flex"; ``compile_attention`` is accepted
   and ignored (nothing is traced or compiled at run time).
+* ``DocPlans(doc_ids)`` is the mask as the native kernels consume it -- their
+  tile plans, built on first use and cached -- for any batch of packs and
+  without the FlexAttention tables (a training step that never hands its mask
+  to FlexAttention has no reader for them).
 * ``eager_attention(q, k, v, doc_ids)`` (attention.py:66-95) keeps the
   reference's per-document SDPA loop for callers that ask for
   ``backend="eager"``; the native path never calls it.
@@ -122,6 +126,21 @@ def build_doc_block_mask(doc_ids: torch.Tensor, n_heads: int, block_size: int = 
     )
 
 
+class DocPlans:
+    """The document mask of ``doc_ids`` [B, S] (any B) for the native kernels only:
+    holds the int64 doc ids and caches the kernels' tile plans per head shape."""
+
+    def __init__(self, doc_ids: torch.Tensor) -> None:
+        N.require_device(doc_ids, op="DocPlans")
+        d = doc_ids.to(torch.int64)
+        if d.dim() == 1:
+            d = d[None]
+        if d.dim() != 2:
+            raise ValueError("doc_ids must be [S] or [B, S]")
+        self.doc_ids = d.contiguous()
+        self._plans: dict = {}
+
+
 # ---------------------------------------------------------------- native attention
 FWD, BWD_KV, BWD_Q = 0, 1, 2
 
@@ -170,7 +189,7 @@ def _plans(doc: torch.Tensor, hq: int, hkv: int, head_dim: int, block_mask) -> d
     # The model passes the very doc_ids tensor the mask was built from; the
     # mask keeps it alive, so pointer identity is a sync-free cache key.
     cache = None
-    if (isinstance(block_mask, DocBlockMask) and block_mask.doc_ids.shape == doc.shape
+    if (isinstance(block_mask, (DocBlockMask, DocPlans)) and block_mask.doc_ids.shape == doc.shape
             and block_mask.doc_ids.data_ptr() == doc.data_ptr()):
         cache = block_mask._plans
     key = ("plans", hq, hkv, head_dim)

@@ -5,6 +5,15 @@ pack of the step (one micro-batch each) build the document block mask, run
 the forward and ``(loss / step_tokens).backward()`` under bf16 autocast; then
 ``clip_grad_norm_(1.0)`` and a fused AdamW step.
 
+The step's gradient is the sum of the packs' gradients, however the packs are
+grouped into micro-batches, so ``packs_per_micro_batch`` > 1 runs several
+packs as one [k, S] batch (one forward and one backward over k*S tokens:
+GEMMs k times taller, a k-times larger attention grid, k times fewer
+launches) -- the same gradient up to the order of fp32 additions.  The
+document mask of a micro-batch is built as the attention kernels' tile plans
+(``DocPlans``); the FlexAttention tables the reference builds for its
+attention have no reader here.
+
 The parameters live in the model's flat store (``FlatParams``): the step
 zeroes the one gradient buffer, runs every micro-batch on one bf16 copy of
 the weights (``hold``), and clips and updates the flat buffer with the fused
@@ -42,7 +51,7 @@ import torch
 
 from packbalance_amd.data.device_packs import DeviceTokenStore, PackBuilder
 from packbalance_amd.model import layers as L
-from packbalance_amd.model.attention import build_doc_block_mask
+from packbalance_amd.model.attention import DocPlans
 from packbalance_amd.model.llama import LlamaForCausalLM
 from packbalance_amd.model.optim import FlatAdamW
 
@@ -50,10 +59,16 @@ from packbalance_amd.model.optim import FlatAdamW
 class TrainStep:
     def __init__(self, cfg, dev, packs_per_step: int = 4, seq_len: int | None = None,
                  seed: int = 0, lr: float = 3e-4, store: DeviceTokenStore | None = None,
-                 streams: int = 1):
+                 streams: int = 1, packs_per_micro_batch: int = 1):
         self.cfg, self.dev = cfg, dev
         seq_len = seq_len or cfg.max_seq_len
-        streams = max(1, min(int(streams), packs_per_step))
+        k = int(packs_per_micro_batch)
+        if k < 1 or packs_per_step % k:
+            raise ValueError(f"packs_per_micro_batch {k} does not divide packs_per_step "
+                             f"{packs_per_step}")
+        self.k = k
+        n_micro = packs_per_step // k
+        streams = max(1, min(int(streams), n_micro))
         torch.manual_seed(seed)
         self.model = LlamaForCausalLM(cfg).to(dev)
         self.model.train()
@@ -64,16 +79,17 @@ class TrainStep:
                              max_grad_norm=1.0, copy_dtype=torch.bfloat16)
 
         def z():
-            return torch.zeros((1, seq_len), dtype=torch.int64, device=dev)
+            return torch.zeros((k, seq_len), dtype=torch.int64, device=dev)
 
         self.builder = None
         if store is not None:
             self.builder = PackBuilder(store, packs_per_step, seq_len)
             out = self.builder.outputs
-            self.static = [{k: out[k][i:i + 1] for k in out} for i in range(packs_per_step)]
+            self.static = [{key: t[j * k:(j + 1) * k] for key, t in out.items()}
+                           for j in range(n_micro)]
         else:
             self.static = [dict(input_ids=z(), labels=z(), position_ids=z(), doc_ids=z())
-                           for _ in range(packs_per_step)]
+                           for _ in range(n_micro)]
         self.step_tokens = torch.ones((), dtype=torch.float32, device=dev)
         self.loss_sum = torch.zeros((), dtype=torch.float32, device=dev)
         self.grad_norm = torch.zeros((), dtype=torch.float32, device=dev)
@@ -95,7 +111,7 @@ class TrainStep:
         self.grad_norm.copy_(self.opt.step())
 
     def _micro_batch(self, b, step_tokens, loss_acc) -> None:
-        bm = build_doc_block_mask(b["doc_ids"], self.cfg.n_heads)
+        bm = DocPlans(b["doc_ids"])
         loss = self.model(b["input_ids"], b["labels"], b["position_ids"], b["doc_ids"],
                           block_mask=bm)
         (loss / step_tokens).backward()
@@ -117,21 +133,22 @@ class TrainStep:
             main.wait_stream(s)
         self.loss_sum.copy_(self.stream_loss.sum())
 
-    @staticmethod
-    def _as_dicts(batch_list):
-        return [dict(input_ids=b.input_ids, labels=b.labels, position_ids=b.position_ids,
-                     doc_ids=b.doc_ids) for b in batch_list]
+    _KEYS = ("input_ids", "labels", "position_ids", "doc_ids")
+
+    def _as_dicts(self, batch_list):
+        """Packs ([1, S] each) grouped into micro-batches of ``k`` ([k, S])."""
+        k = self.k
+        return [{key: torch.cat([getattr(b, key) for b in batch_list[j:j + k]])
+                 for key in self._KEYS} for j in range(0, len(batch_list), k)]
 
     def eager(self, batch_list) -> None:
         tokens = float(sum(b.useful_tokens for b in batch_list))
         self._body(self._as_dicts(batch_list), tokens)
 
     def _load(self, batch_list, tokens_dev) -> None:
-        for dst, b in zip(self.static, batch_list):
-            dst["input_ids"].copy_(b.input_ids)
-            dst["labels"].copy_(b.labels)
-            dst["position_ids"].copy_(b.position_ids)
-            dst["doc_ids"].copy_(b.doc_ids)
+        for dst, src in zip(self.static, self._as_dicts(batch_list)):
+            for key in self._KEYS:
+                dst[key].copy_(src[key])
         self.step_tokens.copy_(tokens_dev)
 
     def capture(self, batch_list, tokens_dev, warmup_steps: int = 2) -> None:

@@ -67,16 +67,18 @@ def _store_tables(cfg, dev, seed=1, n_steps=5):
     return store, steps, tables
 
 
-@pytest.mark.parametrize("streams", [1, 4])
-def test_graph_replays_with_device_packs_match_eager(streams, dev) -> None:
+@pytest.mark.parametrize("streams,packs_per_micro", [(1, 1), (4, 1), (2, 2)])
+def test_graph_replays_with_device_packs_match_eager(streams, packs_per_micro, dev) -> None:
     """The same, with each step's packs built on the device inside the step from a
     token store in HBM (the graph rebuilds them from the table loaded before each
     replay); the eager twin builds them eagerly from the same tables and runs its
-    micro-batches one after another, the graph on ``streams`` streams."""
+    packs one micro-batch after another, the graph ``packs_per_micro`` packs per
+    micro-batch on ``streams`` streams."""
     cfg = cfg1_model()
     store, steps, tables = _store_tables(cfg, dev)
     eager = TrainStep(cfg, dev, seq_len=256, store=store)
-    graph = TrainStep(cfg, dev, seq_len=256, store=store, streams=streams)
+    graph = TrainStep(cfg, dev, seq_len=256, store=store, streams=streams,
+                      packs_per_micro_batch=packs_per_micro)
     graph.capture_packs(tables[0])
     for _ in range(2):
         eager.eager_packs(tables[0])
@@ -115,3 +117,33 @@ def test_concurrent_micro_batches_match_sequential(dev) -> None:
         if i == 0:
             gs, gc = seq.flat.grad, con.flat.grad
             assert (gs - gc).abs().max() <= 1e-5 * gs.abs().max()
+
+
+@pytest.mark.parametrize("packs_per_micro,streams", [(2, 2), (4, 1), (2, 1)])
+def test_multi_pack_micro_batches_match_sequential(packs_per_micro, streams, dev) -> None:
+    """Packs grouped into [k, S] micro-batches give the step's gradient from the
+    same weights.  Unlike concurrent single-pack micro-batches, taller GEMMs
+    change hipBLASLt's tiling and so the fp32 accumulation order inside each
+    bf16-rounded product, which moves gradients by bf16-level amounts: loss to
+    1e-4, gradient norm to 1e-3, gradient entries to 2e-2 of the largest (and
+    their mean absolute difference to 2e-3 of the mean magnitude)."""
+    cfg = cfg1_model()
+    store, _, tables = _store_tables(cfg, dev, seed=3, n_steps=1)
+    seq = TrainStep(cfg, dev, seq_len=256, store=store)
+    grp = TrainStep(cfg, dev, seq_len=256, store=store, streams=streams,
+                    packs_per_micro_batch=packs_per_micro)
+    assert len(grp.static) == 4 // packs_per_micro
+    assert grp.static[0]["input_ids"].shape == (packs_per_micro, 256)
+    seq.eager_packs(tables[0])
+    grp.eager_packs(tables[0])
+    torch.cuda.synchronize()
+    le, lg = float(seq.loss_sum), float(grp.loss_sum)
+    ne, ng = float(seq.grad_norm), float(grp.grad_norm)
+    assert abs(le - lg) <= 1e-4 * abs(le), (le, lg)
+    assert abs(ne - ng) <= 1e-3 * abs(ne), (ne, ng)
+    gs, gg = seq.flat.grad, grp.flat.grad
+    d = (gs - gg).abs()
+    assert d.max() <= 2e-2 * gs.abs().max()
+    assert d.mean() <= 2e-3 * gs.abs().mean()
+    with pytest.raises(ValueError):
+        TrainStep(cfg, dev, seq_len=256, store=store, packs_per_micro_batch=3)
