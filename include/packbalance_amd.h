@@ -319,6 +319,16 @@ int pb_pack_bf16(const void *src, int src_dtype, int64_t src_ld, int64_t rows, i
                  void *dst, int64_t dst_ld, int64_t dst_rows, int64_t dst_cols, int transpose,
                  void *stream);
 
+/* Batched transpose: dst[b][c][r] = src[b][r][c] for b < batch, r < rows,
+ * c < cols; src rows src_row_stride and matrices src_batch_stride elements
+ * apart, dst contiguous [batch, cols, rows]; 2- or 4-byte elements (bits
+ * copied).  No reference counterpart: it writes the transposed weight copies
+ * that the input-gradient GEMMs read (the reference's nn.Linear backward
+ * reads W as stored).                                                       */
+int pb_transpose_batched(const void *src, int64_t src_batch_stride, int64_t src_row_stride,
+                         void *dst, int64_t batch, int64_t rows, int64_t cols, int elem_bytes,
+                         void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -119,9 +119,10 @@ SIGNATURES: dict[str, tuple] = {
         [_pv, _pv, _pv, _pv, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32,
          _i32, _p],
     ),
+    "pb_transpose_batched": (_i32, [_p, _i64, _i64, _p, _i64, _i64, _i64, _i32, _p]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lib: C.CDLL | None = None
 _load_error: str | None = None

@@ -34,6 +34,8 @@ import contextlib
 import torch
 from torch import nn
 
+from packbalance_amd import _native as N
+
 _ALIGN = 64  # elements: every non-grouped parameter and group starts 256-byte aligned
 
 
@@ -149,11 +151,11 @@ class FlatParams:
         for i, g in enumerate(groups):
             if first[i] != first[0] + i * stride or sum(p.shape[0] for p in g) != rows:
                 raise ValueError("transposed(): groups must share a shape and a constant stride")
-        src = buf.as_strided((len(groups), rows, cols), (stride, cols, 1), first[0])
         dst = hit[1] if hit is not None else torch.empty((len(groups), cols, rows), dtype=buf.dtype,
                                                           device=buf.device)
-        with torch.no_grad():
-            dst.copy_(src.transpose(1, 2))
+        N.require_device(buf, op="FlatParams.transposed")
+        N.call("pb_transpose_batched", buf.data_ptr() + first[0] * buf.element_size(), stride, cols,
+               dst.data_ptr(), len(groups), rows, cols, buf.element_size(), N.stream_ptr(buf))
         self._tcache[key] = (self.refreshes, dst)
         return dst
 
