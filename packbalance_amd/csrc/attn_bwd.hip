@@ -401,10 +401,12 @@ void attn_bwd_dkdv_pipe(BwdArgs a) {
 
   // Element mask of a PARTIAL step: same document, kv <= q (q < S always).
   auto mask = [&](f32x16_t &sv, int q0, const int64_t *qd) {
+    int64_t dq[16];
+    lds_docs16(qd, hh, dq);
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const int qr = 8 * (j >> 2) + 4 * hh + (j & 3);
-      const bool ok = kvvalid && kv <= q0 + qr && qd[qr] == kvdoc;
+      const int qr = pi_row(hh, j);
+      const bool ok = kvvalid & (kv <= q0 + qr) & (dq[j] == kvdoc);
       sv[j] = ok ? sv[j] : -INFINITY;
     }
   };
@@ -837,10 +839,12 @@ void attn_bwd_dq_pipe(BwdArgs a) {
   };
   // Element mask of a PARTIAL sub-tile: same document and kv <= q.
   auto mask = [&](f32x16_t &sv, int kv0, const int64_t *kd) {
+    int64_t dkv[16];
+    lds_docs16(kd, hh, dkv);
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const int kr = 8 * (j >> 2) + 4 * hh + (j & 3);
-      const bool ok = qvalid && kv0 + kr <= qi && kd[kr] == qdoc;
+      const int kr = pi_row(hh, j);
+      const bool ok = qvalid & (kv0 + kr <= qi) & (dkv[j] == qdoc);
       sv[j] = ok ? sv[j] : -INFINITY;
     }
   };

@@ -42,6 +42,23 @@ __device__ __forceinline__ f32x16_t zero16() {
 // Row offset (within a 16-row k step) carried by k slot s of lane half h.
 __device__ __forceinline__ int pi_row(int h, int s) { return 8 * (s >> 2) + 4 * h + (s & 3); }
 
+// Document ids of the 16 rows pi_row(hh, j), j = 0..15, of a 32-row
+// sub-tile whose ids sit in LDS (16-byte aligned): four runs of four
+// consecutive ids, read as 16-byte vectors before any of them is compared, so
+// an element mask waits for LDS once rather than once per element.
+__device__ __forceinline__ void lds_docs16(const int64_t *d, int hh, int64_t (&out)[16]) {
+  typedef int64_t i64x2_t __attribute__((ext_vector_type(2)));
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const i64x2_t lo = *reinterpret_cast<const i64x2_t *>(d + 8 * g + 4 * hh);
+    const i64x2_t hi = *reinterpret_cast<const i64x2_t *>(d + 8 * g + 4 * hh + 2);
+    out[4 * g] = lo[0];
+    out[4 * g + 1] = lo[1];
+    out[4 * g + 2] = hi[0];
+    out[4 * g + 3] = hi[1];
+  }
+}
+
 // Eight consecutive head-dim elements of one row, zero beyond `d` (the real
 // head dim) or when the row is out of range.  `vec` = 16-byte path allowed.
 __device__ __forceinline__ bf16x8_t load_row8(const bf16_t *row, int d0, int d, bool valid,

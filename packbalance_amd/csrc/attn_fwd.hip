@@ -391,15 +391,17 @@ void attn_fwd_pipe(FwdArgs a) {
   auto entry = [&](int u) { return lst[(u < U ? u : U - 1) >> 1]; };
   auto row0 = [&](int e, int u) { return plan_tile(e) * kKvStep + 32 * (u & 1); };
 
-  // Element mask of a PARTIAL sub-tile: same document and kv <= q.
+  // Element mask of a PARTIAL sub-tile: same document and kv <= q.  Bitwise
+  // ands keep it branch-free (no per-element exec branch around an LDS read).
   auto mask = [&](f32x16_t (&sv)[NQB], int kv0, const int64_t *kd) {
+    int64_t dkv[16];
+    lds_docs16(kd, hh, dkv);
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const int kr = 8 * (j >> 2) + 4 * hh + (j & 3);
-      const int64_t dkv = kd[kr];
+      const int kr = pi_row(hh, j);
 #pragma unroll
       for (int qb = 0; qb < NQB; ++qb) {
-        const bool ok = qv[qb] && kv0 + kr <= qi[qb] && dkv == qdoc[qb];
+        const bool ok = qv[qb] & (kv0 + kr <= qi[qb]) & (dkv[j] == qdoc[qb]);
         sv[qb][j] = ok ? sv[qb][j] : -INFINITY;
       }
     }
