@@ -400,14 +400,32 @@ void attn_bwd_dkdv_pipe(BwdArgs a) {
   };
 
   // Element mask of a PARTIAL step: same document, kv <= q (q < S always).
-  auto mask = [&](f32x16_t &sv, int q0, const int64_t *qd) {
+  // Tests as bitwise ands (no per-element branch), with two wave-uniform
+  // shortcuts: a step wholly at or after the wave's last KV row needs no
+  // causal test, a CAUSAL plan tile no document test.  KV rows past the
+  // sequence end are left unmasked: their dK / dV are never stored.
+  // kv <= q0 + pi_row(hh, j)  <=>  kv - q0 - 4hh <= 8(j/4) + j%4.
+  const int kvmax = kt * BN + wave * 32 + 31;
+  auto mask = [&](f32x16_t &sv, int e, int q0, const int64_t *qd) {
+    const bool diag = q0 < kvmax;
+    const int rel = kv - q0 - 4 * hh;
+    if (plan_causal(e)) {
+      if (!diag) return;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) sv[j] = rel <= 8 * (j >> 2) + (j & 3) ? sv[j] : -INFINITY;
+      return;
+    }
     int64_t dq[16];
     lds_docs16(qd, hh, dq);
+    if (diag) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int qr = pi_row(hh, j);
-      const bool ok = kvvalid & (kv <= q0 + qr) & (dq[j] == kvdoc);
-      sv[j] = ok ? sv[j] : -INFINITY;
+      for (int j = 0; j < 16; ++j) {
+        const bool ok = (rel <= 8 * (j >> 2) + (j & 3)) & (dq[j] == kvdoc);
+        sv[j] = ok ? sv[j] : -INFINITY;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) sv[j] = dq[j] == kvdoc ? sv[j] : -INFINITY;
     }
   };
 
@@ -462,7 +480,7 @@ void attn_bwd_dkdv_pipe(BwdArgs a) {
       sc = mfma32(rfrag(qs0, dk), kf[dk], sc);
       pc = mfma32(rfrag(gs0, dk), vf[dk], pc);
     }
-    if (!plan_full(e0)) mask(sc, step_of(0, e0).q0, qd0);
+    if (!plan_full(e0)) mask(sc, e0, step_of(0, e0).q0, qd0);
 
     auto body = [&](auto Rc, int t) {
       constexpr int R = decltype(Rc)::value;
@@ -502,7 +520,7 @@ void attn_bwd_dkdv_pipe(BwdArgs a) {
         dvdk(f, cfrag(gslot(IR()), f), cfrag(qslot(IR()), f), pf, dsf);
       sc = sn;
       pc = pn;
-      if (!plan_full(e1)) mask(sc, step_of(t + 1, e1).q0, dslot(IR1()));
+      if (!plan_full(e1)) mask(sc, e1, step_of(t + 1, e1).q0, dslot(IR1()));
       wait_vmcnt<2 * NDMA>();
       block_sync_nofence();
       ew[0] = ew[1];
@@ -838,14 +856,29 @@ void attn_bwd_dq_pipe(BwdArgs a) {
     Dma::copy(Vb, a.v.ss, voff, kv0, vslot(Rc), wave);
   };
   // Element mask of a PARTIAL sub-tile: same document and kv <= q.
-  auto mask = [&](f32x16_t &sv, int kv0, const int64_t *kd) {
+  // Tests and shortcuts as in attn_fwd_pipe (query rows past the sequence end
+  // are left unmasked: their dQ is never stored).
+  const int qmin = qt * BM + wave * 32;
+  auto mask = [&](f32x16_t &sv, int e, int kv0, const int64_t *kd) {
+    const bool diag = kv0 + 31 > qmin;
+    const int rel = qi - kv0 - 4 * hh;
+    if (plan_causal(e)) {
+      if (!diag) return;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) sv[j] = 8 * (j >> 2) + (j & 3) <= rel ? sv[j] : -INFINITY;
+      return;
+    }
     int64_t dkv[16];
     lds_docs16(kd, hh, dkv);
+    if (diag) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int kr = pi_row(hh, j);
-      const bool ok = qvalid & (kv0 + kr <= qi) & (dkv[j] == qdoc);
-      sv[j] = ok ? sv[j] : -INFINITY;
+      for (int j = 0; j < 16; ++j) {
+        const bool ok = (8 * (j >> 2) + (j & 3) <= rel) & (dkv[j] == qdoc);
+        sv[j] = ok ? sv[j] : -INFINITY;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) sv[j] = dkv[j] == qdoc ? sv[j] : -INFINITY;
     }
   };
   typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -877,7 +910,7 @@ void attn_bwd_dq_pipe(BwdArgs a) {
       sc = mfma32(rfrag(ks0, dk), qf[dk], sc);
       pc = mfma32(rfrag(vs0, dk), gf[dk], pc);
     }
-    if (!plan_full(e0)) mask(sc, row0(e0, 0), kd0);
+    if (!plan_full(e0)) mask(sc, e0, row0(e0, 0), kd0);
 
     auto body = [&](auto Rc, int u) {
       constexpr int R = decltype(Rc)::value;
@@ -913,7 +946,7 @@ void attn_bwd_dq_pipe(BwdArgs a) {
         dq_acc[f % NDB] = mfma32(cfrag(kslot(IR()), f), dsf[f / NDB], dq_acc[f % NDB]);
       sc = sn;
       pc = pn;
-      if (!plan_full(e1)) mask(sc, row0(e1, u + 1), dslot(IR1()));
+      if (!plan_full(e1)) mask(sc, e1, row0(e1, u + 1), dslot(IR1()));
       wait_vmcnt<2 * NDMA>();
       block_sync_nofence();
       ew[0] = ew[1];

@@ -243,9 +243,12 @@ __device__ __forceinline__ void decode_q_major(int bid, int nqt, int B, int Hq, 
   h = hk * G + g;
 }
 
-// Packed plan entry: tile index << 1 | FULL flag.
-__device__ __forceinline__ int plan_tile(int e) { return e >> 1; }
-__device__ __forceinline__ bool plan_full(int e) { return e & 1; }
+// Packed plan entry: tile index << 2 | kind, kind 1 = FULL (no element mask),
+// 2 = CAUSAL (every pair with kv <= q in the tile shares a document, so the
+// causal test alone is the mask), 0 = PARTIAL (document and causal tests).
+__device__ __forceinline__ int plan_tile(int e) { return e >> 2; }
+__device__ __forceinline__ bool plan_full(int e) { return (e & 3) == 1; }
+__device__ __forceinline__ bool plan_causal(int e) { return (e & 3) == 2; }
 
 // ---------------------------------------------------------------- host side
 inline int check_attn_shape(const char *what, int64_t b, int64_t hq, int64_t hkv, int64_t s,
@@ -352,8 +355,10 @@ inline int64_t attn_bwd_workspace(int64_t b, int64_t hq, int64_t hkv, int64_t s,
 
 }  // namespace attn
 
-// Classifier shared with the block-table builder (block_tables.hip).
+// Classifier shared with the block-table builder (block_tables.hip): per
+// (pack, q tile, kv tile) 0 = empty, 1 = partial, 2 = full, and, only when
+// causal_class is set, 3 = partial with one document for every pair kv <= q.
 int classify_doc_tiles(const int64_t *doc, int64_t doc_stride, int64_t b, int64_t s, int qbs,
-                       int kbs, uint8_t *cls, hipStream_t st);
+                       int kbs, int causal_class, uint8_t *cls, hipStream_t st);
 
 }  // namespace pb

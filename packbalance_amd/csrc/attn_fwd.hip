@@ -391,19 +391,42 @@ void attn_fwd_pipe(FwdArgs a) {
   auto entry = [&](int u) { return lst[(u < U ? u : U - 1) >> 1]; };
   auto row0 = [&](int e, int u) { return plan_tile(e) * kKvStep + 32 * (u & 1); };
 
-  // Element mask of a PARTIAL sub-tile: same document and kv <= q.  Bitwise
-  // ands keep it branch-free (no per-element exec branch around an LDS read).
-  auto mask = [&](f32x16_t (&sv)[NQB], int kv0, const int64_t *kd) {
+  // Element mask of a non-FULL sub-tile (kv rows kv0 .. kv0+31): same
+  // document and kv <= q, as bitwise tests (no per-element branch).  Two
+  // wave-uniform shortcuts: a sub-tile wholly at or before the wave's first
+  // query row needs no causal test, and a CAUSAL plan tile no document test.
+  // Rows past the sequence end are left unmasked: they are never stored.
+  // kv0 + pi_row(hh, j) <= q  <=>  8(j/4) + j%4 <= q - kv0 - 4hh.
+  const int qmin = qt * BM + wave * MQ;
+  auto mask = [&](f32x16_t (&sv)[NQB], int e, int kv0, const int64_t *kd) {
+    const bool diag = kv0 + 31 > qmin;
+    int rel[NQB];
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) rel[qb] = qi[qb] - kv0 - 4 * hh;
+    if (plan_causal(e)) {
+      if (!diag) return;
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb)
+          sv[qb][j] = 8 * (j >> 2) + (j & 3) <= rel[qb] ? sv[qb][j] : -INFINITY;
+      return;
+    }
     int64_t dkv[16];
     lds_docs16(kd, hh, dkv);
+    if (diag) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int kr = pi_row(hh, j);
+      for (int j = 0; j < 16; ++j)
 #pragma unroll
-      for (int qb = 0; qb < NQB; ++qb) {
-        const bool ok = qv[qb] & (kv0 + kr <= qi[qb]) & (dkv[j] == qdoc[qb]);
-        sv[qb][j] = ok ? sv[qb][j] : -INFINITY;
-      }
+        for (int qb = 0; qb < NQB; ++qb) {
+          const bool ok = (8 * (j >> 2) + (j & 3) <= rel[qb]) & (dkv[j] == qdoc[qb]);
+          sv[qb][j] = ok ? sv[qb][j] : -INFINITY;
+        }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) sv[qb][j] = dkv[j] == qdoc[qb] ? sv[qb][j] : -INFINITY;
     }
   };
 
@@ -515,7 +538,7 @@ void attn_fwd_pipe(FwdArgs a) {
     }
     {
       const int e = entry(0);
-      if (!plan_full(e)) mask(sc, row0(e, 0), kd0);
+      if (!plan_full(e)) mask(sc, e, row0(e, 0), kd0);
     }
     __syncthreads();  // K slot 0 is refilled by body 0
 
@@ -563,7 +586,7 @@ void attn_fwd_pipe(FwdArgs a) {
         pv_step(f, vf[f], pf);
         if (f < NQB) sc[f] = sn[f];
       }
-      if (!plan_full(e1)) mask(sc, row0(e1, u + 1), dslot(IR1()));
+      if (!plan_full(e1)) mask(sc, e1, row0(e1, u + 1), dslot(IR1()));
       // The DMA just issued may stay in flight; everything older (the previous
       // body's DMA, this body's entry load and document DMA) must land.
       wait_vmcnt<2 * NDMA>();

@@ -2,7 +2,8 @@
 //
 // A plan lists, for every row tile of one orientation, the non-empty tiles of
 // the other orientation in ascending order, each tagged FULL (no element mask
-// needed) or PARTIAL.  It is the attention kernels' form of the FlexAttention
+// needed), CAUSAL (one document for every pair with kv <= q: the causal test
+// is the whole mask) or PARTIAL.  It is the attention kernels' form of the FlexAttention
 // block tables (kv_indices / full_kv_indices for by_kv = 0, q_indices /
 // full_q_indices for by_kv = 1), at the kernels' own tile sizes, with FULL and
 // PARTIAL merged into one ascending list so a kernel walks one array.
@@ -11,7 +12,7 @@
 namespace pb {
 namespace {
 
-enum : uint8_t { kEmpty = 0, kPartial = 1, kFull = 2 };
+enum : uint8_t { kEmpty = 0, kPartial = 1, kFull = 2, kCausal = 3 };
 
 __global__ __launch_bounds__(256) void plan_lists(const uint8_t *__restrict__ cls, int nb, int nq,
                                                   int nk, int by_kv, int32_t *__restrict__ counts,
@@ -25,7 +26,7 @@ __global__ __launch_bounds__(256) void plan_lists(const uint8_t *__restrict__ cl
   int n = 0;
   for (int c = 0; c < ncols; ++c) {
     const uint8_t v = by_kv ? C[(int64_t)c * nk + r] : C[(int64_t)r * nk + c];
-    if (v != kEmpty) L[n++] = (c << 1) | (v == kFull ? 1 : 0);
+    if (v != kEmpty) L[n++] = (c << 2) | (v == kFull ? 1 : v == kCausal ? 2 : 0);
   }
   counts[tid] = n;
 }
@@ -44,7 +45,7 @@ extern "C" int pb_attn_plan(const int64_t *doc_ids, int64_t doc_stride, int64_t 
   PB_CHECK_ARG(doc_stride >= s, "pb_attn_plan: doc_stride < s");
   PB_CHECK_ARG(by_kv == 0 || by_kv == 1, "pb_attn_plan: by_kv must be 0 or 1");
   hipStream_t st = as_stream(stream);
-  int rc = classify_doc_tiles(doc_ids, doc_stride, b, s, (int)q_tile, (int)kv_tile, class_ws, st);
+  int rc = classify_doc_tiles(doc_ids, doc_stride, b, s, (int)q_tile, (int)kv_tile, 1, class_ws, st);
   if (rc) return rc;
   const int nq = (int)((s + q_tile - 1) / q_tile), nk = (int)((s + kv_tile - 1) / kv_tile);
   const int64_t rows = b * (by_kv ? nk : nq);

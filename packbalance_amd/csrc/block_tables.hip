@@ -19,12 +19,14 @@
 namespace pb {
 namespace {
 
-enum : uint8_t { kEmpty = 0, kPartial = 1, kFull = 2 };
+enum : uint8_t { kEmpty = 0, kPartial = 1, kFull = 2, kCausal = 3 };
 
 // grid = (nkv, nq, b); block = 256 threads.  qb x kb tile sizes in tokens.
+// With causal_class, a partial tile in which every in-range pair with kv <= q
+// shares a document is reported as kCausal (its mask is the causal test).
 __global__ __launch_bounds__(256) void classify_tiles(const int64_t *__restrict__ doc,
                                                       int64_t doc_stride, int64_t s, int qbs,
-                                                      int kbs, int nq, int nkv,
+                                                      int kbs, int nq, int nkv, int causal_class,
                                                       uint8_t *__restrict__ cls) {
   const int kb = blockIdx.x, qb = blockIdx.y, b = blockIdx.z;
   uint8_t *out = cls + ((int64_t)b * nq + qb) * nkv + kb;
@@ -40,18 +42,22 @@ __global__ __launch_bounds__(256) void classify_tiles(const int64_t *__restrict_
   for (int i = threadIdx.x; i < qbs; i += 256) dq[i] = (q0 + i < s) ? drow[q0 + i] : 0;
   for (int i = threadIdx.x; i < kbs; i += 256) dk[i] = (k0 + i < s) ? drow[k0 + i] : 0;
   __syncthreads();
-  int any = 0, all = 1;
+  int any = 0, all = 1, one_doc = 1;
   const int pairs = qbs * kbs;
   for (int p = threadIdx.x; p < pairs; p += 256) {
     const int i = p / kbs, j = p - (p / kbs) * kbs;
     const int64_t q = q0 + i, kv = k0 + j;
-    const bool ok = q < s && kv < s && q >= kv && dq[i] == dk[j];
-    any |= ok;
-    all &= ok;
+    const bool causal = q < s && kv < s && q >= kv;
+    const bool same = dq[i] == dk[j];
+    any |= causal & same;
+    all &= causal & same;
+    one_doc &= !causal | same;
   }
   any = __syncthreads_or(any);
   all = __syncthreads_and(all);
-  if (threadIdx.x == 0) *out = all ? kFull : (any ? kPartial : kEmpty);
+  one_doc = __syncthreads_and(one_doc);
+  if (threadIdx.x == 0)
+    *out = all ? kFull : !any ? kEmpty : (causal_class && one_doc) ? kCausal : kPartial;
 }
 
 // One thread per (b, h, row) of either orientation.
@@ -116,12 +122,12 @@ __global__ __launch_bounds__(256) void order_tables(const uint8_t *__restrict__ 
 
 // Shared with the attention planner: classify tiles of qbs x kbs tokens.
 int classify_doc_tiles(const int64_t *doc, int64_t doc_stride, int64_t b, int64_t s, int qbs,
-                       int kbs, uint8_t *cls, hipStream_t st) {
+                       int kbs, int causal_class, uint8_t *cls, hipStream_t st) {
   const int nq = (int)((s + qbs - 1) / qbs), nkv = (int)((s + kbs - 1) / kbs);
   dim3 grid(nkv, nq, (unsigned)b);
   const size_t lds = (size_t)(qbs + kbs) * sizeof(int64_t);
   hipLaunchKernelGGL(classify_tiles, grid, dim3(256), lds, st, doc, doc_stride, s, qbs, kbs, nq, nkv,
-                     cls);
+                     causal_class, cls);
   return launch_status("classify_doc_tiles");
 }
 
@@ -142,7 +148,7 @@ extern "C" int pb_doc_block_tables(const int64_t *doc_ids, int64_t doc_stride, i
   const int64_t nblk = (s + block - 1) / block;
   PB_CHECK_SUPPORTED(nblk <= 65535 && b <= 65535, "pb_doc_block_tables: too many blocks");
   hipStream_t st = as_stream(stream);
-  int rc = classify_doc_tiles(doc_ids, doc_stride, b, s, (int)block, (int)block, class_ws, st);
+  int rc = classify_doc_tiles(doc_ids, doc_stride, b, s, (int)block, (int)block, 0, class_ws, st);
   if (rc) return rc;
   const int64_t threads = b * h * (2 * nblk);
   hipLaunchKernelGGL(order_tables, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,

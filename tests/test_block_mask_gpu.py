@@ -87,7 +87,9 @@ def test_build_doc_block_mask_rejects_batch(dev) -> None:
 
 @pytest.mark.parametrize("q_tile,kv_tile,by_kv", [(128, 64, 0), (64, 128, 1), (64, 64, 0), (64, 64, 1)])
 def test_attention_plans_match_oracle(q_tile, kv_tile, by_kv, dev) -> None:
-    """pb_attn_plan lists == the closed-form tile classes, ascending, FULL bit set."""
+    """pb_attn_plan lists == the closed-form tile classes, ascending, each entry
+    tile << 2 | kind: 1 FULL, 2 CAUSAL (a partial tile in which every in-range
+    pair with kv <= q shares a document, checked densely per tile), 0 PARTIAL."""
     from packbalance_amd import _native as N
 
     packs = W.cfg3_packs()[:3] + [[5000, 3000, 192]]
@@ -102,11 +104,27 @@ def test_attention_plans_match_oracle(q_tile, kv_tile, by_kv, dev) -> None:
     N.call("pb_attn_plan", doc.data_ptr(), doc.stride(0), b, s, q_tile, kv_tile, by_kv,
            counts.data_ptr(), lists.data_ptr(), ws.data_ptr(), N.stream_ptr(doc))
     counts, lists = counts.cpu().numpy(), lists.cpu().numpy()
+
+    def one_doc(d, qi, kj):  # every in-range pair with kv <= q shares a document
+        qa = np.arange(qi * q_tile, min((qi + 1) * q_tile, s))
+        ka = np.arange(kj * kv_tile, min((kj + 1) * kv_tile, s))
+        causal = qa[:, None] >= ka[None, :]
+        return bool(np.all((d[qa][:, None] == d[ka][None, :])[causal]))
+
+    kinds = set()
     for i in range(b):
-        cls = OB.classify_closed(doc[i].cpu().numpy(), q_tile, kv_tile)
-        if by_kv:
-            cls = cls.T
+        d = doc[i].cpu().numpy()
+        cls = OB.classify_closed(d, q_tile, kv_tile)
         for r in range(rows):
-            want = [(c << 1) | int(cls[r, c] == OB.FULL) for c in range(cols) if cls[r, c]]
+            want = []
+            for c in range(cols):
+                qi, kj = (c, r) if by_kv else (r, c)
+                k = cls[qi, kj]
+                if k == OB.FULL:
+                    want.append((c << 2) | 1)
+                elif k == OB.PARTIAL:
+                    want.append((c << 2) | (2 if one_doc(d, qi, kj) else 0))
+            kinds.update(w & 3 for w in want)
             assert counts[i, r] == len(want), (i, r)
             assert lists[i, r, : len(want)].tolist() == want, (i, r)
+    assert kinds == {0, 1, 2}
