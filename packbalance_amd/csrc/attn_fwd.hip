@@ -241,15 +241,18 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
 // sub-tiles are copied global -> LDS by DMA (global_load_lds_dwordx4) into
 // the swizzled layout, through 3-slot rings (slot = u % 3, compile-time in the
 // 3x unrolled loop), one barrier per sub-tile.  Body u issues the DMA of
-// K(u+3) and V(u+2), then runs an explicit software pipeline: for each of the
-// DP/16 head-dim steps of S(u+1) = K(u+1) Q^T it issues that step's MFMAs and
-// a fixed slice of the online softmax of S(u) (max, then exponentials), in
-// that order (sched_barrier fences keep the compiler from regrouping them),
-// so the VALU work runs under the MFMAs.  O^T += V(u)^T P(u)^T follows, with
-// the V fragments already read during the softmax steps.  The body finally
-// waits only for the DMA issued one body earlier.  The running max moves
-// only when a sub-tile's max exceeds it by more than kTau (log2 units), so
-// the O rescale is a rare wave-uniform branch and P stays below 2^kTau.
+// K(u+3) and V(u+1), then runs a three-stage software pipeline over the DP/16
+// head-dim steps: step k issues the k-th MFMA of S(u+1) = K(u+1) Q^T, the
+// k-th MFMA of O^T += V(u-1)^T P(u-1)^T (P of the previous sub-tile, kept in
+// registers) and a fixed slice of the online softmax of S(u) (max, then
+// exponentials), in that order (sched_barrier fences keep the compiler from
+// regrouping them).  Every step thus pairs two MFMAs with an even share of
+// the VALU work, and no MFMA waits for a result of its own body.  The body
+// ends with the O rescale for the new running max (after PV(u-1), which was
+// relative to the old one) and waits only for the DMA it issued.  The
+// running max moves only when a sub-tile's max exceeds it by more than kTau
+// (log2 units), so the rescale is a rare wave-uniform branch and P stays
+// below 2^kTau.
 template <int DP, int MQ, int WAVES>
 __global__ __launch_bounds__(64 * WAVES)
 __attribute__((amdgpu_waves_per_eu(MQ == 64 ? 1 : 2, MQ == 64 ? 1 : 2)))
@@ -261,12 +264,11 @@ void attn_fwd_pipe(FwdArgs a) {
   constexpr int NDMA = Dma::NDMA;
   constexpr float kTau = 8.0f;
   // Softmax schedule over the NDK steps: step 0 row max, step 1 lane-pair
-  // max and new running max, steps 2.. the 8*NQB exponential pairs.
+  // max and new running max, steps 2 .. NDK-1 the 8*NQB exponential pairs
+  // (pair p in step 2 + p (NDK-2) / NPAIR).
   constexpr int NPAIR = 8 * NQB;
-  constexpr int PPS = (NPAIR + NDK - 3) / (NDK - 2);
-  constexpr int NVF = 2 * NDB;                    // V fragments per sub-tile
-  constexpr int VPS = (NVF + NDK / 2 - 1) / (NDK / 2);  // read in steps NDK/2..
-  static_assert(NDK >= 4, "head dim");
+  constexpr int NVF = 2 * NDB;  // V fragments per sub-tile: one PV MFMA per step
+  static_assert(NDK >= 4 && NVF == NDK, "head dim");
   // Ring slots are separate LDS objects so that the compiler can tell a
   // fragment read of one slot from the DMA still in flight into another (it
   // would otherwise wait for all outstanding DMA before every read).
@@ -462,7 +464,8 @@ void attn_fwd_pipe(FwdArgs a) {
       }
     } else {
 #pragma unroll
-      for (int p = (step - 2) * PPS; p < (step - 1) * PPS && p < NPAIR; ++p) {
+      for (int p = 0; p < NPAIR; ++p) {
+        if (2 + p * (NDK - 2) / NPAIR != step) continue;
         const int qb = p / 8, j = 2 * (p % 8);
         // The row sum takes the fp32 values (as the reference's softmax does);
         // only the PV operand is rounded to bf16.
@@ -513,7 +516,7 @@ void attn_fwd_pipe(FwdArgs a) {
 
   f32x16_t sc[NQB];
   if (U > 0) {
-    // Prologue: K(0..2), V(0..1) and their documents, then S(0).  U >= 2.
+    // Prologue: K(0..2), V(0) and their documents, then S(0).  U >= 2.
     int ew[4];  // entries of sub-tiles u+1 .. u+4 for body u (see below)
 #pragma unroll
     for (int i = 0; i < 4; ++i) ew[i] = entry(i + 1);
@@ -521,7 +524,7 @@ void attn_fwd_pipe(FwdArgs a) {
       const int e = entry(u);
       load_kdoc(row0(e, u), dslot(Rc));
       Dma::copy(Kb, a.k_ss, koff, row0(e, u), kslot(Rc), wave);
-      if (decltype(Rc)::value < 2) Dma::copy(Vb, a.v_ss, voff, row0(e, u), vslot(Rc), wave);
+      if (decltype(Rc)::value == 0) Dma::copy(Vb, a.v_ss, voff, row0(e, u), vslot(Rc), wave);
     };
     prefetch(I0(), 0);
     prefetch(I1(), 1);
@@ -542,15 +545,23 @@ void attn_fwd_pipe(FwdArgs a) {
     }
     __syncthreads();  // K slot 0 is refilled by body 0
 
-    // Body u (u + 1 < U), ring slot R = u % 3.
+    // P(u-1) between bodies (the first body has no previous sub-tile).
+    bf16x8_t pfp[NQB][2];
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) pfp[qb][0] = pfp[qb][1] = bf16x8_t{};
+
+    // Body u (u + 1 < U), ring slot R = u % 3; PV = false for u = 0 only.
     // Every body issues the same DMA (past the last sub-tile, entry() repeats
     // it into a slot nobody reads any more), so the number of operations in
     // flight -- and the vmcnt to wait for -- is the same in every body.
-    auto body = [&](auto Rc, int u) {
+    // Slots in body u: K(u+3) -> R (K(u) was read in body u-1), K(u+1) read
+    // from R+1; V(u+1) -> R+1 (V(u-2) was read in body u-1), V(u-1) read from
+    // R+2; documents of u+3 -> R, of u+1 read from R+1.
+    auto body = [&](auto Rc, auto PVc, int u) {
       constexpr int R = decltype(Rc)::value;
       constexpr int R1 = (R + 1) % 3, R2 = (R + 2) % 3;
+      constexpr bool PV = decltype(PVc)::value;
       const int e1 = __builtin_amdgcn_readfirstlane(ew[0]);
-      const int e2 = __builtin_amdgcn_readfirstlane(ew[1]);
       const int e3 = __builtin_amdgcn_readfirstlane(ew[2]);
       const int e4 = entry(u + 5);  // for body u + 1, issued before this body's DMA
       __builtin_amdgcn_sched_barrier(0);
@@ -559,10 +570,14 @@ void attn_fwd_pipe(FwdArgs a) {
       using IR2 = std::integral_constant<int, R2>;
       load_kdoc(row0(e3, u + 3), dslot(IR()));
       Dma::copy(Kb, a.k_ss, koff, row0(e3, u + 3), kslot(IR()), wave);
-      Dma::copy(Vb, a.v_ss, voff, row0(e2, u + 2), vslot(IR2()), wave);
+      Dma::copy(Vb, a.v_ss, voff, row0(e1, u + 1), vslot(IR1()), wave);
       bf16x8_t kf[NDK], vf[NVF], pf[NQB][2];
 #pragma unroll
       for (int dk = 0; dk < NDK; ++dk) kf[dk] = kfrag(kslot(IR1()), dk);
+      if constexpr (PV) {
+#pragma unroll
+        for (int f = 0; f < NVF; ++f) vf[f] = vfrag_of(f, vslot(IR2()));
+      }
       f32x16_t sn[NQB];
 #pragma unroll
       for (int qb = 0; qb < NQB; ++qb) sn[qb] = zero16();
@@ -571,20 +586,16 @@ void attn_fwd_pipe(FwdArgs a) {
       for (int dk = 0; dk < NDK; ++dk) {
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb) sn[qb] = mfma32(kf[dk], qf[qb][dk], sn[qb]);
+        if constexpr (PV) pv_step(dk, vf[dk], pfp);
         softmax_step(dk, sc, pf);
-        if (dk >= NDK / 2) {
-#pragma unroll
-          for (int f = (dk - NDK / 2) * VPS; f < (dk - NDK / 2 + 1) * VPS && f < NVF; ++f)
-            vf[f] = vfrag_of(f, vslot(IR()));
-        }
         __builtin_amdgcn_sched_barrier(0);
       }
-      softmax_commit();
-      // O^T += V(u)^T P(u)^T, with S(u+1) moved into sc alongside.
+      softmax_commit();  // rescales O after PV(u-1), which used the old max
 #pragma unroll
-      for (int f = 0; f < NVF; ++f) {
-        pv_step(f, vf[f], pf);
-        if (f < NQB) sc[f] = sn[f];
+      for (int qb = 0; qb < NQB; ++qb) {
+        sc[qb] = sn[qb];
+        pfp[qb][0] = pf[qb][0];
+        pfp[qb][1] = pf[qb][1];
       }
       if (!plan_full(e1)) mask(sc, e1, row0(e1, u + 1), dslot(IR1()));
       // The DMA just issued may stay in flight; everything older (the previous
@@ -596,30 +607,40 @@ void attn_fwd_pipe(FwdArgs a) {
       ew[2] = ew[3];
       ew[3] = e4;
     };
-    int u = 0;
+    using NoPV = std::false_type;
+    using WithPV = std::true_type;
+    body(I0(), NoPV(), 0);
+    int u = 1;
     for (; u + 3 < U; u += 3) {
-      body(I0(), u);
-      body(I1(), u + 1);
-      body(I2(), u + 2);
+      body(I1(), WithPV(), u);
+      body(I2(), WithPV(), u + 1);
+      body(I0(), WithPV(), u + 2);
     }
     if (u + 1 < U) {
-      body(I0(), u);
+      body(I1(), WithPV(), u);
       ++u;
     }
     if (u + 1 < U) {
-      body(I1(), u);
+      body(I2(), WithPV(), u);
       ++u;
     }
-    wait_vmcnt<0>();  // the repeated DMA of the last bodies
-    // Last sub-tile: no S(u+1); its V sits in slot u % 3.
-    const int rl = u % 3;
-    const char *vt = rl == 0 ? vs0 : rl == 1 ? vs1 : vs2;
-    bf16x8_t pf[NQB][2];
+    // V(u) of the last sub-tile u = U-1 was issued by the last body: every
+    // wave's share must land before any wave reads it.
+    wait_vmcnt<0>();
+    __syncthreads();
+    auto vslot_rt = [&](int r) -> const char * { return r == 0 ? vs0 : r == 1 ? vs1 : vs2; };
+    const char *vprev = vslot_rt((u + 2) % 3), *vlast = vslot_rt(u % 3);
+    bf16x8_t vf[NVF], pf[NQB][2];
 #pragma unroll
-    for (int step = 0; step < NDK; ++step) softmax_step(step, sc, pf);
+    for (int f = 0; f < NVF; ++f) vf[f] = vfrag_of(f, vprev);
+#pragma unroll
+    for (int step = 0; step < NDK; ++step) {
+      pv_step(step, vf[step], pfp);
+      softmax_step(step, sc, pf);
+    }
     softmax_commit();
 #pragma unroll
-    for (int f = 0; f < NVF; ++f) pv_step(f, vfrag_of(f, vt), pf);
+    for (int f = 0; f < NVF; ++f) pv_step(f, vfrag_of(f, vlast), pf);
   }
 
 #pragma unroll
