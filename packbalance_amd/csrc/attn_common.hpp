@@ -154,13 +154,31 @@ __device__ __forceinline__ bf16x8_t swz_col_frag(const char *tile, int k0, int c
   return *reinterpret_cast<bf16x8_t *>(&r);
 }
 
-// Copy ROWS rows (kv0.., DP columns of a [rows][ss] bf16 view at byte address
-// `base`) into a swizzled LDS tile with global_load_lds_dwordx4: lane i of a
+// Raw-buffer resource word 3 on gfx9-family parts (32-bit data, no swizzle).
+constexpr int kBufWord3 = 0x00020000;
+
+// LDS DMA of 16 bytes per active lane: lane i copies bytes [voff, voff + 16)
+// after `base` (wave-uniform) to LDS bytes [16i, 16i + 16) of `dst`.  Issued
+// as a raw buffer load with num_records = `limit` bytes (reads past it return
+// zeros instead of faulting).  The compiler counts buffer LDS loads in vmcnt
+// only; a FLAT global_load_lds in flight makes it wait for every outstanding
+// LDS read (lgkmcnt(0)) wherever it waits for one.
+__device__ __forceinline__ void dma16(const void *base, int64_t limit, uint32_t voff, void *dst) {
+  const int lim = (int)(limit < 0x7fffffff ? limit : 0x7fffffff);
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, lim, kBufWord3);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)dst, 16,
+                                           voff, 0, 0, 0);
+}
+
+// Copy ROWS rows (kv0.., DP columns of a [S][ss] bf16 view at byte address
+// `base`) into a swizzled LDS tile by LDS DMA (dma16): lane i of a
 // wave-level instruction writes LDS bytes [16i, 16i+16) of its 1 KiB slice,
 // so each lane fetches the global chunk that the swizzle puts there.
 // `off[i]` = byte offset of that chunk within the tile (precomputed per
-// thread).  The caller guarantees kv0 + ROWS <= sequence length.  Every
-// thread issues exactly NDMA instructions; completion is tracked by vmcnt.
+// thread).  The caller guarantees kv0 + ROWS <= S; the buffer bound is the
+// end of row S-1.  Every thread issues exactly NDMA instructions; completion
+// is tracked by vmcnt.
 template <int DP, int ROWS, int NT>
 struct TileDma {
   static constexpr int NDMA = ROWS * DP * 2 / 16 / NT;
@@ -174,14 +192,12 @@ struct TileDma {
     }
   }
   __device__ static __forceinline__ void copy(const char *base, int64_t ss, const uint32_t *off,
-                                              int kv0, char *dst, int wave) {
+                                              int kv0, int S, char *dst, int wave) {
     const char *tb = base + (int64_t)kv0 * ss * 2;
+    const int64_t limit = ((int64_t)(S - 1 - kv0) * ss + DP) * 2;
     constexpr int W = NT / 64;
 #pragma unroll
-    for (int i = 0; i < NDMA; ++i)
-      __builtin_amdgcn_global_load_lds(
-          tb + off[i], (__attribute__((address_space(3))) void *)(dst + (i * W + wave) * 1024), 16,
-          0, 0);
+    for (int i = 0; i < NDMA; ++i) dma16(tb, limit, off[i], dst + (i * W + wave) * 1024);
   }
 };
 

@@ -238,7 +238,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
 // registers, one wave per SIMD and AGPR<->VGPR copies, and measured slower
 // (2.34 vs 1.94 ms on 8 x 8192-token packs, 32/8 heads, D 128).
 // The KV tiles of the plan are walked as 32-row sub-tiles u.  K and V
-// sub-tiles are copied global -> LDS by DMA (global_load_lds_dwordx4) into
+// sub-tiles are copied global -> LDS by DMA (buffer_load_dwordx4 ... lds) into
 // the swizzled layout, through 3-slot rings (slot = u % 3, compile-time in the
 // 3x unrolled loop), one barrier per sub-tile.  Body u issues the DMA of
 // K(u+3) and V(u+1), then runs a three-stage software pipeline over the DP/16
@@ -269,6 +269,7 @@ void attn_fwd_pipe(FwdArgs a) {
   constexpr int NPAIR = 8 * NQB;
   constexpr int NVF = 2 * NDB;  // V fragments per sub-tile: one PV MFMA per step
   static_assert(NDK >= 4 && NVF == NDK, "head dim");
+  constexpr int kAhead = 4;  // steps whose K / V fragments are read before the first MFMA
   // Ring slots are separate LDS objects so that the compiler can tell a
   // fragment read of one slot from the DMA still in flight into another (it
   // would otherwise wait for all outstanding DMA before every read).
@@ -509,9 +510,7 @@ void attn_fwd_pipe(FwdArgs a) {
   // kdoc of sub-tile rows kv0..kv0+31 into a ring slot: one DMA instruction
   // by 16 lanes of wave 0 (issued for every sub-tile, read for PARTIAL ones).
   auto load_kdoc = [&](int kv0, int64_t *dst) {
-    if (wave == 0 && lane < 16)
-      __builtin_amdgcn_global_load_lds(docb + kv0 + 2 * lane,
-                                       (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+    if (wave == 0 && lane < 16) dma16(docb + kv0, (int64_t)(S - kv0) * 8, 16 * lane, dst);
   };
 
   f32x16_t sc[NQB];
@@ -523,8 +522,8 @@ void attn_fwd_pipe(FwdArgs a) {
     auto prefetch = [&](auto Rc, int u) {
       const int e = entry(u);
       load_kdoc(row0(e, u), dslot(Rc));
-      Dma::copy(Kb, a.k_ss, koff, row0(e, u), kslot(Rc), wave);
-      if (decltype(Rc)::value == 0) Dma::copy(Vb, a.v_ss, voff, row0(e, u), vslot(Rc), wave);
+      Dma::copy(Kb, a.k_ss, koff, row0(e, u), S, kslot(Rc), wave);
+      if (decltype(Rc)::value == 0) Dma::copy(Vb, a.v_ss, voff, row0(e, u), S, vslot(Rc), wave);
     };
     prefetch(I0(), 0);
     prefetch(I1(), 1);
@@ -569,15 +568,19 @@ void attn_fwd_pipe(FwdArgs a) {
       using IR1 = std::integral_constant<int, R1>;
       using IR2 = std::integral_constant<int, R2>;
       load_kdoc(row0(e3, u + 3), dslot(IR()));
-      Dma::copy(Kb, a.k_ss, koff, row0(e3, u + 3), kslot(IR()), wave);
-      Dma::copy(Vb, a.v_ss, voff, row0(e1, u + 1), vslot(IR1()), wave);
+      Dma::copy(Kb, a.k_ss, koff, row0(e3, u + 3), S, kslot(IR()), wave);
+      Dma::copy(Vb, a.v_ss, voff, row0(e1, u + 1), S, vslot(IR1()), wave);
+      // Fragments in the order the steps consume them: steps 0 .. kAhead-1
+      // before the first MFMA, step k + kAhead during step k, so at most 12
+      // LDS reads are outstanding and each MFMA waits only for its own
+      // operands (the LGKM counter tracks 15; more forces a full drain).
       bf16x8_t kf[NDK], vf[NVF], pf[NQB][2];
+      auto read_step = [&](int k) {
+        kf[k] = kfrag(kslot(IR1()), k);
+        if constexpr (PV) vf[k] = vfrag_of(k, vslot(IR2()));
+      };
 #pragma unroll
-      for (int dk = 0; dk < NDK; ++dk) kf[dk] = kfrag(kslot(IR1()), dk);
-      if constexpr (PV) {
-#pragma unroll
-        for (int f = 0; f < NVF; ++f) vf[f] = vfrag_of(f, vslot(IR2()));
-      }
+      for (int k = 0; k < kAhead; ++k) read_step(k);
       f32x16_t sn[NQB];
 #pragma unroll
       for (int qb = 0; qb < NQB; ++qb) sn[qb] = zero16();
@@ -587,6 +590,7 @@ void attn_fwd_pipe(FwdArgs a) {
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb) sn[qb] = mfma32(kf[dk], qf[qb][dk], sn[qb]);
         if constexpr (PV) pv_step(dk, vf[dk], pfp);
+        if (dk + kAhead < NDK) read_step(dk + kAhead);
         softmax_step(dk, sc, pf);
         __builtin_amdgcn_sched_barrier(0);
       }
