@@ -52,56 +52,77 @@ __device__ __forceinline__ void store_vec(T *p, const float (&v)[N]) {
 }
 
 // ---------------------------------------------------------------- forward
-// Register-resident row: NV vectors of VEC elements per lane.
+// Register-resident row: NV vectors of VEC elements per lane.  Each wave walks
+// rows wave_id, wave_id + total_waves, ... and loads the next row while it
+// reduces and writes the current one, so a wave keeps a row of reads in
+// flight at all times; w is loaded once per wave and kept packed.
 template <typename TX, typename TW, int NV>
 __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_reg(
     const TX *__restrict__ x, int64_t xs, const TW *__restrict__ w, TX *__restrict__ y, int64_t ys,
     float *__restrict__ rstd_out, int64_t rows, int n, float eps) {
   constexpr int VEC = 16 / sizeof(TX);
+  constexpr int WB = VEC * sizeof(TW);  // bytes of w per vector
+  typedef unsigned wraw_t __attribute__((ext_vector_type(WB / 4)));
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  const int64_t step = (int64_t)gridDim.x * kWaves;
+  int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const TX *xr = x + row * xs;
-  // x is streamed (non-temporal: read once); w is re-read by every row and
-  // stays cached.  All loads are issued before the reduction.
-  u32x4 raw[NV];
-  float wv[NV][VEC];
+  wraw_t wraw[NV];
+  u32x4 cur[NV];
+  auto load_row = [&](int64_t r, u32x4 (&dst)[NV]) {
+    const TX *xr = x + r * xs;
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int c = (i * 64 + lane) * VEC;
-    if (c < n) {
-      raw[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(xr + c));
-      load_vec<TW, VEC>(w + c, wv[i]);
+    for (int i = 0; i < NV; ++i) {
+      const int c = (i * 64 + lane) * VEC;
+      if (c < n) dst[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(xr + c));
     }
-  }
-  float v[NV][VEC];
-  float ss = 0.f;
+  };
+  load_row(row, cur);
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = (i * 64 + lane) * VEC;
-    if (c < n) {
-      const TX *e = reinterpret_cast<const TX *>(&raw[i]);
+    if (c < n) wraw[i] = *reinterpret_cast<const wraw_t *>(w + c);
+  }
+#pragma unroll 1
+  for (; row < rows; row += step) {
+    u32x4 nxt[NV];
+    if (row + step < rows) load_row(row + step, nxt);
+    float ss = 0.f;
 #pragma unroll
-      for (int k = 0; k < VEC; ++k) {
-        v[i][k] = to_f32(e[k]);
-        ss += v[i][k] * v[i][k];
+    for (int i = 0; i < NV; ++i) {
+      const int c = (i * 64 + lane) * VEC;
+      if (c < n) {
+        const TX *e = reinterpret_cast<const TX *>(&cur[i]);
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) ss += to_f32(e[k]) * to_f32(e[k]);
       }
     }
-  }
-  ss = wave_sum(ss);
-  const float r = 1.0f / sqrtf(ss / (float)n + eps);
-  if (lane == 0) rstd_out[row] = r;
-  TX *yr = y + row * ys;
+    ss = wave_sum(ss);
+    const float r = 1.0f / sqrtf(ss / (float)n + eps);
+    if (lane == 0) rstd_out[row] = r;
+    TX *yr = y + row * ys;
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int c = (i * 64 + lane) * VEC;
-    if (c < n) {
-      float o[VEC];
+    for (int i = 0; i < NV; ++i) {
+      const int c = (i * 64 + lane) * VEC;
+      if (c < n) {
+        const TX *e = reinterpret_cast<const TX *>(&cur[i]);
+        const TW *we = reinterpret_cast<const TW *>(&wraw[i]);
+        float o[VEC];
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) o[e] = v[i][e] * r * wv[i][e];
-      store16_nt<TX>(yr + c, o);
+        for (int k = 0; k < VEC; ++k) o[k] = to_f32(e[k]) * r * to_f32(we[k]);
+        store16_nt<TX>(yr + c, o);
+      }
     }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) cur[i] = nxt[i];
   }
+}
+
+// Workgroups of the register-resident forward: enough for four 4-wave
+// workgroups per CU (rows walked in a loop beyond that).
+inline unsigned fwd_reg_grid(int64_t rows) {
+  const int64_t want = (rows + kWaves - 1) / kWaves;
+  return (unsigned)(want < 1024 ? want : 1024);
 }
 
 // General row (any n, any alignment): two passes over the row, scalar loads.
@@ -357,8 +378,8 @@ int fwd_typed(const void *x, int64_t xs, const void *w, void *y, int64_t ys, flo
   switch (nv) {
 #define PB_FWD(NV)                                                                               \
   case NV:                                                                                       \
-    hipLaunchKernelGGL((rmsnorm_fwd_reg<TX, TW, NV>), grid, dim3(kThreads), 0, st, X, xs, W, Y,  \
-                       ys, rstd, rows, (int)n, eps);                                             \
+    hipLaunchKernelGGL((rmsnorm_fwd_reg<TX, TW, NV>), dim3(fwd_reg_grid(rows)), dim3(kThreads), \
+                       0, st, X, xs, W, Y, ys, rstd, rows, (int)n, eps);                         \
     break;
     PB_FWD(1) PB_FWD(2) PB_FWD(4) PB_FWD(8)
 #undef PB_FWD
