@@ -185,3 +185,28 @@ def test_attention_cfg3_pack(pack, dev) -> None:
     _close(dk[sl, g : g + 1], ref["dk"], "dk")
     _close(dv[sl, g : g + 1], ref["dv"], "dv")
     assert torch.isfinite(out.float()).all() and torch.isfinite(dq.float()).all()
+
+
+@pytest.mark.parametrize("layout", ["mixed", "noncontiguous"])
+def test_attention_large_grid_layouts(layout, dev) -> None:
+    """A large-grid D 128 shape (>= 2048 query tiles per launch, no KV split) with
+    long and single-token documents and a padded tail, or document ids that
+    recur in several runs; every head of one KV group is checked in full
+    against the oracle."""
+    S, Hq, Hkv, D = 8192, 32, 8, 128
+    if layout == "mixed":
+        doc = W.doc_ids_from_lengths([[3000, 1, 1, 700, 64, 1990, 33, 2000]], S)  # 403 pad
+    else:
+        doc = torch.tensor([[(i // 300) % 5 for i in range(S)]])
+    doc = doc.to(dev)
+    q, k, v, do = _inputs(1, Hq, Hkv, S, D, dev, seed=21)
+    out, dq, dk, dv = _run(q, k, v, do, doc)
+    g = 3
+    hs = slice(4 * g, 4 * g + 4)
+    ref = OA.attention(q[:, hs], k[:, g : g + 1], v[:, g : g + 1], doc.cpu(), do[:, hs],
+                       dtype=torch.float32)
+    _close(out[:, hs], ref["out"], "out")
+    _close(dq[:, hs], ref["dq"], "dq")
+    _close(dk[:, g : g + 1], ref["dk"], "dk")
+    _close(dv[:, g : g + 1], ref["dv"], "dv")
+    assert torch.isfinite(out.float()).all()
