@@ -110,6 +110,17 @@ int pb_ce_rows(const void *logits, int64_t stride_m, int64_t stride_v,
                void *dlogits, int64_t m, int64_t v, int64_t ignore_index,
                float z_loss_coeff, void *stream);
 
+/* pb_ce_rows with dlogits of its own dtype and strides (the same values,
+ * rounded once to dl_dtype), e.g. fp32 logits from a GEMM with fp32 output
+ * and the bf16 dlogits a gradient GEMM consumes, in one pass.  Extends
+ * _ce_launch (fused_ce.py:91-118), whose dlogits is always
+ * empty_like(logits).                                                       */
+int pb_ce_rows_dl(const void *logits, int64_t stride_m, int64_t stride_v,
+                  int dtype, const int64_t *targets, float *loss, float *lse_out,
+                  void *dlogits, int64_t dl_stride_m, int64_t dl_stride_v,
+                  int dl_dtype, int64_t m, int64_t v, int64_t ignore_index,
+                  float z_loss_coeff, void *stream);
+
 /* ---- Document block tables (FlexAttention BlockMask layout) -------------
  * Replaces packbalance/model/attention.py:25-54 (build_doc_block_mask) with
  * torch.nn.attention.flex_attention.create_block_mask's table semantics:

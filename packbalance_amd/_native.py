@@ -66,6 +66,8 @@ SIGNATURES: dict[str, tuple] = {
     "pb_swiglu_bwd_rows": (_i32, [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _i64,
                                   _i32, _p]),
     "pb_ce_rows": (_i32, [_p, _i64, _i64, _i32, _p, _p, _p, _p, _i64, _i64, _i64, _f32, _p]),
+    "pb_ce_rows_dl": (_i32, [_p, _i64, _i64, _i32, _p, _p, _p, _p, _i64, _i64, _i32, _i64, _i64,
+                             _i64, _f32, _p]),
     "pb_doc_block_tables": (
         _i32,
         [_p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p],

@@ -39,10 +39,12 @@ def use_triton(x: torch.Tensor) -> bool:
 
 
 def ce_rows(logits: torch.Tensor, targets: torch.Tensor, *, write_dlogits: bool,
-            ignore_index: int = -100, z_loss_coeff: float = 0.0):
+            ignore_index: int = -100, z_loss_coeff: float = 0.0,
+            dlogits_dtype: torch.dtype | None = None):
     """Per-row CE of a logits block: returns (loss fp32 [M], lse fp32 [M], dlogits | None).
 
-    dlogits has the dtype and strides of ``logits`` (``torch.empty_like``).
+    dlogits has the dtype and strides of ``logits`` (``torch.empty_like``), or
+    is a contiguous tensor of ``dlogits_dtype`` when that is given.
     """
     N.require_device(logits, targets, op="ce_rows")
     if logits.dim() != 2:
@@ -53,18 +55,22 @@ def ce_rows(logits: torch.Tensor, targets: torch.Tensor, *, write_dlogits: bool,
         raise ValueError(f"logits has {m} rows but targets has {t.numel()}")
     t = t.to(torch.int64).contiguous()
     dl = None
-    if write_dlogits:
+    if write_dlogits and dlogits_dtype is not None:
+        dl = torch.empty((m, v), dtype=dlogits_dtype, device=logits.device)
+    elif write_dlogits:
         dl = torch.empty_like(logits)
         if dl.stride() != logits.stride():  # non-dense view: the kernel shares strides
             logits = logits.contiguous()
             dl = torch.empty_like(logits)
     loss = torch.empty(m, dtype=torch.float32, device=logits.device)
     lse = torch.empty(m, dtype=torch.float32, device=logits.device)
+    dls = dl.stride() if dl is not None else logits.stride()
     N.call(
-        "pb_ce_rows",
+        "pb_ce_rows_dl",
         logits.data_ptr(), logits.stride(0), logits.stride(1), N.dtype_code(logits),
-        t.data_ptr(), loss.data_ptr(), lse.data_ptr(), N.ptr(dl),
-        m, v, int(ignore_index), float(z_loss_coeff), N.stream_ptr(logits),
+        t.data_ptr(), loss.data_ptr(), lse.data_ptr(), N.ptr(dl), dls[0], dls[1],
+        N.dtype_code(dl if dl is not None else logits), m, v, int(ignore_index),
+        float(z_loss_coeff), N.stream_ptr(logits),
     )
     return loss, lse, dl
 

@@ -30,7 +30,9 @@ def _case(m, v, dtype, dev, *, seed=0, scale=1.0, ignore_every=0, transposed=Fal
     "m,v,dtype,z,transposed",
     [
         (64, 128, torch.float32, 0.0, False),
-        (37, 32000, torch.float32, 0.0, False),  # model vocab, streaming path
+        (37, 32000, torch.float32, 0.0, False),  # model vocab, 1024-thread register rows
+        (7, 40000, torch.bfloat16, 0.0, False),  # 1024-thread register rows, bf16
+        (5, 33000, torch.float32, 0.0, False),  # beyond the register rows: streaming
         (16, 8192, torch.bfloat16, 0.0, False),  # register path (cfg4 chunk width)
         (16, 8192, torch.bfloat16, 0.01, False),
         (9, 1000, torch.bfloat16, 0.01, True),  # strided vocab axis
@@ -52,6 +54,32 @@ def test_ce_rows_matches_oracle(m, v, dtype, z, transposed, dev) -> None:
     ignored = (t == -100).cpu()
     assert float(loss.cpu()[ignored].abs().sum()) == 0.0
     assert float(dl.cpu()[ignored].abs().sum()) == 0.0
+
+
+@pytest.mark.parametrize(
+    "m,v,dtype,transposed",
+    [
+        (41, 32000, torch.float32, False),  # the library-GEMM CE block: fp32 in, bf16 out
+        (6, 1000, torch.float32, False),  # 256-thread register rows
+        (4, 33000, torch.float32, False),  # streaming
+        (9, 1000, torch.float32, True),  # strided logits, contiguous dlogits
+        (8, 4096, torch.bfloat16, False),  # bf16 in, fp32 out (32-byte stores)
+    ],
+)
+def test_ce_rows_dlogits_dtype(m, v, dtype, transposed, dev) -> None:
+    """dlogits in its own dtype: the same values as the oracle's, rounded once."""
+    logits, t = _case(m, v, dtype, dev, seed=3, ignore_every=4, transposed=transposed, scale=3.0)
+    out = torch.float32 if dtype == torch.bfloat16 else torch.bfloat16
+    loss, lse, dl = ce_rows(logits, t, write_dlogits=True, z_loss_coeff=0.01, dlogits_dtype=out)
+    l_ref, lse_ref, dl_ref = OK.ce_rows(logits, t, z_loss_coeff=0.01)
+    torch.testing.assert_close(loss.cpu().double(), l_ref, rtol=1e-4, atol=1e-4)
+    torch.testing.assert_close(lse.cpu().double(), lse_ref, rtol=1e-4, atol=1e-4)
+    assert dl.dtype == out and dl.is_contiguous() and dl.shape == (m, v)
+    tol = 1e-5 if out == torch.float32 else 1e-2
+    torch.testing.assert_close(dl.cpu().double(), dl_ref, rtol=tol, atol=tol)
+    if out == torch.bfloat16:  # one rounding of the fp32 value
+        same, _, dl32 = ce_rows(logits, t, write_dlogits=True, z_loss_coeff=0.01)
+        assert torch.equal(dl, dl32.to(torch.bfloat16)) and torch.equal(same, loss)
 
 
 def test_ce_rows_cfg4_chunk(dev) -> None:
