@@ -22,6 +22,7 @@
 #include <math.h>
 
 #include "common.hpp"
+#include "lds_dma.hpp"
 
 namespace pb {
 namespace ce {
@@ -94,10 +95,320 @@ __device__ __forceinline__ void store_out(void *out, int dtype, int64_t idx, flo
     static_cast<f16_t *>(out)[idx] = (f16_t)v;
 }
 
-// kDlogits stages its bf16 tile [BM][TP] (vocab-major) in the operand LDS
-// after the main loop, so both dlogits layouts leave as 16-byte stores.
-constexpr int TP = BN + 8;  // staging row pitch (elements): 272 bytes
-static_assert(BM * TP * 2 <= 2 * BM * AP * 2, "staging tile must fit the operand LDS");
+// ---------------------------------------------------------------- DMA GEMM
+// gemm_nt_dma: the product for K-slices that are whole multiples of 64, on
+// tiles of WM x WN waves, each wave 32*IM x 32*JN (IM x JN MFMA blocks).  The
+// A and B K-slices arrive by LDS DMA (16-byte buffer loads, rows past M / N
+// read as zero) in the swizzled 128-byte-row layout of SwzTile<64>
+// (conflict-free ds_read_b128 fragments, no padding), through a ring of
+// STAGES slices: the slices STAGES-1 steps ahead are in flight while one is
+// computed, with a single barrier per slice.  Workgroup i runs on XCD i % 8;
+// each XCD takes a contiguous range of tiles in groups of kGroupM tile rows,
+// so the workgroups resident on one XCD share A and B panels in its L2.
+// gemm_nt (below) is the register-staged kernel for every other shape.
+constexpr int kGroupM = 8;
+
+__device__ __forceinline__ void tile_of(int id, int ntm, int ntn, int &tm, int &tn) {
+  const int total = ntm * ntn;
+  if (total % 8 == 0) id = (id % 8) * (total / 8) + id / 8;
+  const int group = id / (kGroupM * ntn), first = group * kGroupM;
+  const int rows = min(kGroupM, ntm - first);
+  const int local = id - group * kGroupM * ntn;
+  tm = first + local % rows;
+  tn = local / rows;
+}
+
+// Epilogue of a finished tile (both kernels), WM x WN waves of 64*WM*WN
+// threads: acc[i][j] of wave (wm, wn) = (wave / WN, wave % WN) holds rows
+// m0 + 32*IM*wm + 32i + 8(r/4) + 4hh + r%4 and column n0 + 32*JN*wn + 32j + l32.
+// kDlogits stages its bf16 rows (vocab-major, pitch BN + 8) in `stage`, one
+// wave row (32*IM rows) at a time, so both dlogits layouts leave as 16-byte
+// stores; the caller has finished every read of `stage` as an operand buffer.
+template <int MODE, int WM, int WN, int IM, int JN>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs &g, f32x16_t (&acc)[IM][JN], int tm,
+                                              int m0, int n0, bf16_t *stage,
+                                              float (*red_m)[32 * JN * WN],
+                                              float (*red_s)[32 * JN * WN]) {
+  constexpr int NT = 64 * WM * WN, BNT = 32 * JN * WN, WR = 32 * IM, WC = 32 * JN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hh = lane >> 5, l32 = lane & 31;
+  const int wm = wave / WN, wn = wave % WN;
+  if constexpr (MODE == kLse) {
+    static_assert(NT >= BNT, "one thread per token column");
+#pragma unroll
+    for (int j = 0; j < JN; ++j) {
+      const int nl = WC * wn + 32 * j + l32;
+      const int n = n0 + nl;
+      const bool nvalid = n < g.N;
+      const int64_t t = nvalid ? g.targets[n] : g.ignore_index;
+      const bool valid = nvalid && t != g.ignore_index;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < IM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + WR * wm + 32 * i + 8 * (r >> 2) + 4 * hh + (r & 3);
+          if (m < g.M) {
+            mx = fmaxf(mx, acc[i][j][r]);
+            if (valid && (int64_t)(g.v0 + m) == t) g.tgt[n] = acc[i][j][r];
+          }
+        }
+      mx *= kLog2e;
+      float sm = 0.f;
+#pragma unroll
+      for (int i = 0; i < IM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + WR * wm + 32 * i + 8 * (r >> 2) + 4 * hh + (r & 3);
+          if (m < g.M) sm += fast_exp2(acc[i][j][r] * kLog2e - mx);
+        }
+      const float mo = __shfl_xor(mx, 32), so = __shfl_xor(sm, 32);
+      const float mn = fmaxf(mx, mo);
+      if (mn != -INFINITY) sm = sm * fast_exp2(mx - mn) + so * fast_exp2(mo - mn);
+      if (hh == 0) {
+        red_m[wm][nl] = mn;
+        red_s[wm][nl] = sm;
+      }
+    }
+    __syncthreads();
+    if (tid < BNT) {
+      const int n = n0 + tid;
+      float m1 = red_m[0][tid], s1 = red_s[0][tid];
+#pragma unroll
+      for (int w = 1; w < WM; ++w) {
+        const float m2 = red_m[w][tid], s2 = red_s[w][tid];
+        const float mn = fmaxf(m1, m2);
+        if (mn != -INFINITY) s1 = s1 * fast_exp2(m1 - mn) + s2 * fast_exp2(m2 - mn);
+        m1 = mn;
+      }
+      if (n < g.N) {
+        g.part_m[(int64_t)tm * g.N + n] = m1;
+        g.part_s[(int64_t)tm * g.N + n] = s1;
+      }
+    }
+  } else if constexpr (MODE == kDlogits) {
+    static_assert(BNT == 128, "dlogits staging assumes 128 tokens per tile");
+    static_assert((WR * 16) % NT == 0, "staging rows split evenly over the threads");
+    constexpr int TPS = BNT + 8;  // staging row pitch (elements)
+    constexpr int TG = NT / BNT;  // token-row groups per store sweep
+    float lse2[JN], scale[JN], one[JN];
+    int64_t tj[JN];
+#pragma unroll
+    for (int j = 0; j < JN; ++j) {
+      const int n = n0 + WC * wn + 32 * j + l32;
+      const bool nvalid = n < g.N;
+      tj[j] = nvalid ? g.targets[n] : g.ignore_index;
+      const bool valid = nvalid && tj[j] != g.ignore_index;
+      const float lse = nvalid ? g.lse[n] : 0.f;
+      lse2[j] = lse * kLog2e;
+      scale[j] = valid ? (*g.grad_out) * (1.0f + 2.0f * g.z * lse) : 0.f;
+      one[j] = valid ? (*g.grad_out) : 0.f;
+    }
+    for (int pass = 0; pass < WM; ++pass) {
+      __syncthreads();  // the staging rows are free
+      if (wm == pass) {
+#pragma unroll
+        for (int j = 0; j < JN; ++j) {
+          const int nl = WC * wn + 32 * j + l32;
+          const bool nvalid = n0 + nl < g.N;
+#pragma unroll
+          for (int i = 0; i < IM; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int ml = 32 * i + 8 * (r >> 2) + 4 * hh + (r & 3);
+              const int m = m0 + WR * pass + ml;
+              float gv = fast_exp2(acc[i][j][r] * kLog2e - lse2[j]) * scale[j];
+              if ((int64_t)(g.v0 + m) == tj[j]) gv -= one[j];
+              stage[ml * TPS + nl] = (bf16_t)(m < g.M && nvalid ? gv : 0.f);
+            }
+        }
+      }
+      __syncthreads();
+      const int mb = m0 + WR * pass;
+      // dL^T [vocab][tokens]: 16 threads per 256-byte staging row.
+#pragma unroll
+      for (int k = 0; k < WR * 16 / NT; ++k) {
+        const int c = tid + NT * k;
+        const int ml = c >> 4, n8 = (c & 15) * 8;
+        if (mb + ml < g.M && n0 + n8 < g.N)
+          *reinterpret_cast<u32x4 *>(g.dlt + (int64_t)(mb + ml) * g.ldlt + n0 + n8) =
+              *reinterpret_cast<const u32x4 *>(&stage[ml * TPS + n8]);
+      }
+      // dL [tokens][vocab]: lane <-> token, eight vocab rows per 16-byte store.
+#pragma unroll
+      for (int k = 0; k < WR * 16 / NT; ++k) {
+        const int nl = tid & (BNT - 1), m8 = 8 * ((tid / BNT) + TG * k);
+        if (n0 + nl < g.N && mb + m8 < g.M) {
+          bf16x8_t v;
+#pragma unroll
+          for (int x = 0; x < 8; ++x) v[x] = stage[(m8 + x) * TPS + nl];
+          *reinterpret_cast<bf16x8_t *>(g.dl + (int64_t)(n0 + nl) * g.ldl + mb + m8) = v;
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < IM; ++i)
+#pragma unroll
+      for (int j = 0; j < JN; ++j) {
+        const int n = n0 + WC * wn + 32 * j + l32;
+        if (n >= g.N) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + WR * wm + 32 * i + 8 * (r >> 2) + 4 * hh + (r & 3);
+          if (m >= g.M) continue;
+          float v = acc[i][j][r];
+          if constexpr (MODE == kAccum) {
+            if (g.part) {
+              g.part[((int64_t)blockIdx.y * g.M + m) * g.N + n] = v;
+              continue;
+            }
+            float *p = g.acc + (int64_t)m * g.ldc + n;
+            if (!g.first) v += *p;
+            if (g.last)
+              store_out(g.out, g.out_dtype, (int64_t)m * g.ldo + n, v);
+            else
+              *p = v;
+          } else {
+            if (MODE == kStore && g.accum_out) {
+              static_cast<float *>(g.out)[(int64_t)m * g.ldo + n] += v;
+              continue;
+            }
+            store_out(g.out, g.out_dtype, (int64_t)m * g.ldo + n, v);
+          }
+        }
+      }
+  }
+}
+
+// Tile shape of one DMA-kernel instantiation.
+template <int WM_, int WN_, int IM_, int JN_, int STAGES_>
+struct DmaShape {
+  static constexpr int WM = WM_, WN = WN_, IM = IM_, JN = JN_, STAGES = STAGES_;
+  static constexpr int NT = 64 * WM * WN, BMT = 32 * IM * WM, BNT = 32 * JN * WN;
+};
+
+template <int MODE, class SH>
+__global__ __launch_bounds__(SH::NT) void gemm_nt_dma(GemmArgs g) {
+  constexpr int WM = SH::WM, WN = SH::WN, IM = SH::IM, JN = SH::JN, STAGES = SH::STAGES;
+  constexpr int NT = SH::NT, BMT = SH::BMT, BNT = SH::BNT, W = NT / 64;
+  constexpr int WR = 32 * IM, WC = 32 * JN;
+  constexpr int AB = BMT * 128, SB = AB + BNT * 128;  // bytes of one stage (A then B)
+  constexpr int NA = AB / (16 * NT), NB = BNT * 128 / (16 * NT);  // DMAs per thread per stage
+  static_assert(NA * 16 * NT == AB && NB * 16 * NT == BNT * 128, "stage / thread mismatch");
+  static_assert(STAGES == 2 || STAGES == 3, "ring of 2 or 3 slices");
+  static_assert(MODE != kDlogits || WR * (BNT + 8) * 2 <= SB, "dlogits staging must fit a stage");
+  // Stages are separate LDS objects, so the compiler does not wait for the
+  // DMA into one before reading another.
+  __shared__ __align__(16) char st0[SB], st1[SB], st2[STAGES == 3 ? SB : 16];
+  __shared__ float red_m[MODE == kLse ? WM : 1][BNT], red_s[MODE == kLse ? WM : 1][BNT];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hh = lane >> 5, l32 = lane & 31;
+  const int wm = wave / WN, wn = wave % WN;
+  const int ntm = (g.M + BMT - 1) / BMT, ntn = (g.N + BNT - 1) / BNT;
+  int tm, tn;
+  tile_of((int)blockIdx.x, ntm, ntn, tm, tn);
+  const int m0 = tm * BMT, n0 = tn * BNT;
+  const int kb = MODE == kAccum && g.part ? blockIdx.y * g.k_per_split : 0;
+  const int ke = MODE == kAccum && g.part ? min(g.K, kb + g.k_per_split) : g.K;
+  const int nk = (ke - kb) / 64;  // >= 1, checked by the host
+
+  // DMA: chunk p of a stage <- row r, 16-byte chunk c of the K-slice.
+  uint32_t aoff[NA], boff[NB];
+#pragma unroll
+  for (int i = 0; i < NA; ++i) {
+    int r, c;
+    SwzTile<64>::at((i * W + wave) * 64 + lane, r, c);
+    aoff[i] = (uint32_t)((r * g.lda + c * 8) * 2);
+  }
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    int r, c;
+    SwzTile<64>::at((i * W + wave) * 64 + lane, r, c);
+    boff[i] = (uint32_t)((r * g.ldb + c * 8) * 2);
+  }
+  const char *abase = reinterpret_cast<const char *>(g.A + (int64_t)m0 * g.lda + kb);
+  const char *bbase = reinterpret_cast<const char *>(g.B + (int64_t)n0 * g.ldb + kb);
+  // Valid bytes from the slice-0 base: through row M-1 (N-1), column ke.
+  const int64_t alim = ((int64_t)(g.M - 1 - m0) * g.lda + (ke - kb)) * 2;
+  const int64_t blim = ((int64_t)(g.N - 1 - n0) * g.ldb + (ke - kb)) * 2;
+  // Slices past the last reload the last one into a slot nobody reads again,
+  // so every step waits for the same DMA count.
+  auto dma = [&](int t, char *dst) {
+    const int64_t ko = (int64_t)(t < nk ? t : nk - 1) * 128;
+#pragma unroll
+    for (int i = 0; i < NA; ++i) dma16(abase + ko, alim - ko, aoff[i], dst + (i * W + wave) * 1024);
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+      dma16(bbase + ko, blim - ko, boff[i], dst + AB + (i * W + wave) * 1024);
+  };
+  // Fragment offsets: rows WR*wm + 32i + l32 of A, WC*wn + 32j + l32 of B,
+  // 16-byte chunk 2ks + hh.  The swizzle depends on the row only through
+  // l32 (the row offsets are multiples of 16 lines), so row blocks differ by
+  // 32 rows = 4 KiB.
+  int aof[4], bof[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    aof[ks] = SwzTile<64>::off(WR * wm + l32, 16 * ks + 8 * hh);
+    bof[ks] = AB + SwzTile<64>::off(WC * wn + l32, 16 * ks + 8 * hh);
+  }
+
+  f32x16_t acc[IM][JN];
+#pragma unroll
+  for (int i = 0; i < IM; ++i)
+#pragma unroll
+    for (int j = 0; j < JN; ++j) acc[i][j] = zero16();
+
+  auto compute = [&](const char *sb) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      bf16x8_t a[IM], b[JN];
+#pragma unroll
+      for (int i = 0; i < IM; ++i)
+        a[i] = *reinterpret_cast<const bf16x8_t *>(sb + aof[ks] + 4096 * i);
+#pragma unroll
+      for (int j = 0; j < JN; ++j)
+        b[j] = *reinterpret_cast<const bf16x8_t *>(sb + bof[ks] + 4096 * j);
+#pragma unroll
+      for (int i = 0; i < IM; ++i)
+#pragma unroll
+        for (int j = 0; j < JN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+  };
+  // One step: slice kt (in `cur`) has landed for this thread, the barrier
+  // makes it visible and frees `nxt` (slice kt-1's), which takes kt+STAGES-1.
+  auto step = [&](int kt, const char *cur, char *nxt) {
+    wait_vmcnt<(STAGES - 2) * (NA + NB)>();
+    block_sync_nofence();
+    dma(kt + STAGES - 1, nxt);
+    compute(cur);
+  };
+  int kt = 0;
+  if constexpr (STAGES == 3) {
+    dma(0, st0);
+    dma(1, st1);
+    for (; kt + 3 <= nk; kt += 3) {
+      step(kt, st0, st2);
+      step(kt + 1, st1, st0);
+      step(kt + 2, st2, st1);
+    }
+    if (kt < nk) step(kt, st0, st2);
+    if (kt + 1 < nk) step(kt + 1, st1, st0);
+  } else {
+    dma(0, st0);
+    for (; kt + 2 <= nk; kt += 2) {
+      step(kt, st0, st1);
+      step(kt + 1, st1, st0);
+    }
+    if (kt < nk) step(kt, st0, st1);
+  }
+  wait_vmcnt<0>();
+  __syncthreads();  // every wave is done with the stages (kDlogits stages in st0)
+  gemm_epilogue<MODE, WM, WN, IM, JN>(g, acc, tm, m0, n0, reinterpret_cast<bf16_t *>(st0), red_m,
+                                      red_s);
+}
 
 template <int MODE>
 __global__ __launch_bounds__(256) void gemm_nt(GemmArgs g) {
@@ -171,138 +482,7 @@ __global__ __launch_bounds__(256) void gemm_nt(GemmArgs g) {
     }
   }
 
-  // C layout: block (i, j), register r -> row m = 64wm + 32i + 8(r/4) + 4hh + r%4,
-  // column n = 64wn + 32j + l32.
-  if constexpr (MODE == kLse || MODE == kDlogits) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int nl = 64 * wn + 32 * j + l32;
-      const int n = n0 + nl;
-      const bool nvalid = n < g.N;
-      const int64_t t = nvalid ? g.targets[n] : g.ignore_index;
-      const bool valid = t != g.ignore_index;
-      if constexpr (MODE == kLse) {
-        float mx = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int m = m0 + 64 * wm + 32 * i + 8 * (r >> 2) + 4 * hh + (r & 3);
-            const float x = acc[i][j][r];
-            if (m < g.M) {
-              mx = fmaxf(mx, x);
-              if (valid && nvalid && (int64_t)(g.v0 + m) == t) g.tgt[n] = x;
-            }
-          }
-        mx *= kLog2e;
-        float sm = 0.f;
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int m = m0 + 64 * wm + 32 * i + 8 * (r >> 2) + 4 * hh + (r & 3);
-            if (m < g.M) sm += fast_exp2(acc[i][j][r] * kLog2e - mx);
-          }
-        // Merge the two lane halves (other 4-row groups), then the two wave rows.
-        const float mo = __shfl_xor(mx, 32), so = __shfl_xor(sm, 32);
-        const float mn = fmaxf(mx, mo);
-        if (mn != -INFINITY) sm = sm * fast_exp2(mx - mn) + so * fast_exp2(mo - mn);
-        mx = mn;
-        if (hh == 0) {
-          red_m[wm][nl] = mx;
-          red_s[wm][nl] = sm;
-        }
-      } else {
-        // dlogits of this lane's token into the staging tile (vocab-major);
-        // padding rows / columns (m >= M, n >= N) hold 0.
-        if (j == 0) __syncthreads();  // every wave is done with the operand LDS
-        const float lse = nvalid ? g.lse[n] : 0.f;
-        const float lse2 = lse * kLog2e;
-        const float scale = valid ? (*g.grad_out) * (1.0f + 2.0f * g.z * lse) : 0.f;
-        const float one = valid ? (*g.grad_out) : 0.f;
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int ml = 64 * wm + 32 * i + 8 * (r >> 2) + 4 * hh + (r & 3);
-            const int m = m0 + ml;
-            float gv = fast_exp2(acc[i][j][r] * kLog2e - lse2) * scale;
-            if ((int64_t)(g.v0 + m) == t) gv -= one;
-            smem[ml * TP + nl] = (bf16_t)(m < g.M && nvalid ? gv : 0.f);
-          }
-      }
-    }
-    if constexpr (MODE == kDlogits) {
-      __syncthreads();
-      // dL^T [vocab][tokens]: 16 threads per 256-byte staging row.
-#pragma unroll
-      for (int k = 0; k < BM * (BN / 8) / 256; ++k) {
-        const int c = tid + 256 * k;
-        const int ml = c >> 4, n8 = (c & 15) * 8;
-        if (m0 + ml < g.M && n0 + n8 < g.N)
-          *reinterpret_cast<u32x4 *>(g.dlt + (int64_t)(m0 + ml) * g.ldlt + n0 + n8) =
-              *reinterpret_cast<const u32x4 *>(&smem[ml * TP + n8]);
-      }
-      // dL [tokens][vocab]: lane <-> token (conflict-free column reads), eight
-      // vocab rows per 16-byte store.
-#pragma unroll
-      for (int k = 0; k < (BM / 8) * BN / 256; ++k) {
-        const int nl = tid & (BN - 1), m8 = 8 * ((tid >> 7) + 2 * k);
-        if (n0 + nl < g.N && m0 + m8 < g.M) {
-          bf16x8_t v;
-#pragma unroll
-          for (int x = 0; x < 8; ++x) v[x] = smem[(m8 + x) * TP + nl];
-          *reinterpret_cast<bf16x8_t *>(g.dl + (int64_t)(n0 + nl) * g.ldl + m0 + m8) = v;
-        }
-      }
-    }
-    if constexpr (MODE == kLse) {
-      __syncthreads();
-      if (tid < BN) {
-        const int n = n0 + tid;
-        float m1 = red_m[0][tid], s1 = red_s[0][tid];
-        const float m2 = red_m[1][tid], s2 = red_s[1][tid];
-        const float mn = fmaxf(m1, m2);
-        if (mn != -INFINITY) s1 = s1 * fast_exp2(m1 - mn) + s2 * fast_exp2(m2 - mn);
-        if (n < g.N) {
-          g.part_m[(int64_t)tm * g.N + n] = mn;
-          g.part_s[(int64_t)tm * g.N + n] = s1;
-        }
-      }
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int n = n0 + 64 * wn + 32 * j + l32;
-        if (n >= g.N) continue;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int m = m0 + 64 * wm + 32 * i + 8 * (r >> 2) + 4 * hh + (r & 3);
-          if (m >= g.M) continue;
-          float v = acc[i][j][r];
-          if constexpr (MODE == kAccum) {
-            if (g.part) {
-              g.part[((int64_t)blockIdx.y * g.M + m) * g.N + n] = v;
-              continue;
-            }
-            float *p = g.acc + (int64_t)m * g.ldc + n;
-            if (!g.first) v += *p;
-            if (g.last)
-              store_out(g.out, g.out_dtype, (int64_t)m * g.ldo + n, v);
-            else
-              *p = v;
-          } else {
-            if (MODE == kStore && g.accum_out) {
-              static_cast<float *>(g.out)[(int64_t)m * g.ldo + n] += v;
-              continue;
-            }
-            store_out(g.out, g.out_dtype, (int64_t)m * g.ldo + n, v);
-          }
-        }
-      }
-  }
+  gemm_epilogue<MODE, 2, 2, 2, 2>(g, acc, tm, m0, n0, smem, red_m, red_s);
 }
 
 // out (+)= sum of the split-K partials (the kAccum epilogue, applied after a
@@ -410,6 +590,17 @@ __global__ __launch_bounds__(256) void pack_bf16(const T *__restrict__ src, int6
 
 unsigned tiles(int m, int n) { return (unsigned)(((m + BM - 1) / BM) * ((n + BN - 1) / BN)); }
 
+// Tile shape of the DMA kernel: 256 x 128 on 8 waves (two per SIMD), a
+// three-slice ring of 48 KiB slices.  Smaller tiles need more bytes per flop
+// and a 2-slice ring does not cover the operand latency (measured slower).
+using RowShape = DmaShape<4, 2, 2, 2, 3>;
+template <class SH> unsigned dma_tiles(int m, int n) {
+  return (unsigned)(((m + SH::BMT - 1) / SH::BMT) * ((n + SH::BNT - 1) / SH::BNT));
+}
+// The DMA kernel takes K-slices of whole 64-element blocks (operands are
+// already 16-byte aligned with row strides % 8 == 0).
+bool dma_ok(int64_t k) { return k > 0 && k % 64 == 0; }
+
 }  // namespace ce
 }  // namespace pb
 
@@ -481,7 +672,9 @@ extern "C" int pb_lmhead_ce_fwd(const void *x, int64_t ldx, const void *w, int64
     hipLaunchKernelGGL(sum_rows, dim3(1), dim3(1024), 0, st, (const float *)nullptr, 0, loss_sum);
     return launch_status("pb_lmhead_ce_fwd(empty)");
   }
-  const int nmt = (int)((v + BM - 1) / BM);
+  const bool dma = dma_ok(d);
+  const int bm = dma ? RowShape::BMT : BM;  // vocab rows per tile = lse partials per token
+  const int nmt = (int)((v + bm - 1) / bm);
   float *ws = static_cast<float *>(workspace);
   GemmArgs g = {};
   g.A = static_cast<const bf16_t *>(w);
@@ -496,7 +689,11 @@ extern "C" int pb_lmhead_ce_fwd(const void *x, int64_t ldx, const void *w, int64
   g.part_m = ws;
   g.part_s = ws + (int64_t)nmt * n;
   g.tgt = ws + 2 * (int64_t)nmt * n;
-  hipLaunchKernelGGL(gemm_nt<kLse>, dim3(tiles(g.M, g.N)), dim3(256), 0, st, g);
+  if (dma)
+    hipLaunchKernelGGL((gemm_nt_dma<kLse, RowShape>), dim3(dma_tiles<RowShape>(g.M, g.N)),
+                       dim3(RowShape::NT), 0, st, g);
+  else
+    hipLaunchKernelGGL(gemm_nt<kLse>, dim3(tiles(g.M, g.N)), dim3(256), 0, st, g);
   int rc = launch_status("pb_lmhead_ce_fwd(gemm)");
   if (rc) return rc;
   hipLaunchKernelGGL(lse_combine, dim3((unsigned)((n + 63) / 64)), dim3(1024), 0, st, g.part_m,
@@ -523,8 +720,9 @@ BwdWs bwd_ws(int64_t n, int64_t v, int64_t d, int64_t vchunk) {
   w.off_dlt = al(n * vchunk * 2);
   w.off_acc = w.off_dlt + al(vchunk * w.ldlt * 2);
   w.off_part = w.off_acc + al(n * d * 4);
-  // Split the dx GEMM's K (vocab chunk) when its tile grid cannot fill the GPU.
-  const int64_t tiles = ((n + pb::ce::BM - 1) / pb::ce::BM) * ((d + pb::ce::BN - 1) / pb::ce::BN);
+  // Split the dx GEMM's K (vocab chunk) when its tile grid (counted in the
+  // DMA kernel's 256 x 128 tiles) cannot fill the GPU.
+  const int64_t tiles = ((n + 255) / 256) * ((d + 127) / 128);
   int64_t splits = (512 + tiles - 1) / tiles;
   const int64_t kmin = 1024;
   if (splits > vchunk / kmin) splits = vchunk / kmin;
@@ -594,7 +792,11 @@ extern "C" int pb_lmhead_ce_bwd(const void *x, int64_t ldx, const void *w, int64
     g.dlt = dlt;
     g.ldl = ldl;
     g.ldlt = ldlt;
-    hipLaunchKernelGGL(gemm_nt<kDlogits>, dim3(tiles(g.M, g.N)), dim3(256), 0, st, g);
+    if (dma_ok(d))
+      hipLaunchKernelGGL((gemm_nt_dma<kDlogits, RowShape>), dim3(dma_tiles<RowShape>(g.M, g.N)),
+                         dim3(RowShape::NT), 0, st, g);
+    else
+      hipLaunchKernelGGL(gemm_nt<kDlogits>, dim3(tiles(g.M, g.N)), dim3(256), 0, st, g);
     int rc = launch_status("pb_lmhead_ce_bwd(dlogits)");
     if (rc) return rc;
     // 2) dx (+)= dL W_chunk: A = dL [n][vc], B = W^T[:, v0:v0+vc] rows d.
@@ -614,7 +816,11 @@ extern "C" int pb_lmhead_ce_bwd(const void *x, int64_t ldx, const void *w, int64
     gx.part = part;
     gx.k_per_split = L.k_per_split;
     const int splits = part ? (vc + L.k_per_split - 1) / L.k_per_split : 1;
-    hipLaunchKernelGGL(gemm_nt<kAccum>, dim3(tiles(gx.M, gx.N), splits), dim3(256), 0, st, gx);
+    if (dma_ok(vc))
+      hipLaunchKernelGGL((gemm_nt_dma<kAccum, RowShape>), dim3(dma_tiles<RowShape>(gx.M, gx.N), splits),
+                         dim3(RowShape::NT), 0, st, gx);
+    else
+      hipLaunchKernelGGL(gemm_nt<kAccum>, dim3(tiles(gx.M, gx.N), splits), dim3(256), 0, st, gx);
     if (part) {
       const int64_t cnt = (int64_t)gx.M * gx.N;
       hipLaunchKernelGGL(split_reduce, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, st, gx,
@@ -631,7 +837,11 @@ extern "C" int pb_lmhead_ce_bwd(const void *x, int64_t ldx, const void *w, int64
     gw.ldo = lddw;
     gw.out_dtype = dw_dtype;
     gw.accum_out = dw_accumulate != 0;
-    hipLaunchKernelGGL(gemm_nt<kStore>, dim3(tiles(gw.M, gw.N)), dim3(256), 0, st, gw);
+    if (dma_ok(n))
+      hipLaunchKernelGGL((gemm_nt_dma<kStore, RowShape>), dim3(dma_tiles<RowShape>(gw.M, gw.N)),
+                         dim3(RowShape::NT), 0, st, gw);
+    else
+      hipLaunchKernelGGL(gemm_nt<kStore>, dim3(tiles(gw.M, gw.N)), dim3(256), 0, st, gw);
     rc = launch_status("pb_lmhead_ce_bwd(dx/dw)");
     if (rc) return rc;
   }
