@@ -268,7 +268,7 @@ def attention_kernels(dev, iters: int) -> dict:
 def lmhead_ce_kernels(dev, iters: int) -> dict:
     import torch
 
-    from packbalance_amd.kernels.fused_ce import linear_cross_entropy
+    from packbalance_amd.kernels.fused_ce import linear_cross_entropy, vocab_chunk
 
     Nt, V, D = 16384, 128256, 4096
     torch.manual_seed(0)
@@ -297,7 +297,8 @@ def lmhead_ce_kernels(dev, iters: int) -> dict:
     tb /= iters
     flops = 6.0 * Nt * V * D
     return {
-        "workload": "cfg4: x [16384, 4096] bf16, W [128256, 4096] bf16, 1% ignored, vocab chunk 8192",
+        "workload": "cfg4: x [16384, 4096] bf16, W [128256, 4096] bf16, 1% ignored",
+        "vocab_chunk": vocab_chunk(Nt, V),
         "fwd_ms": tf, "bwd_ms": tb,
         "tflops": flops / (tf + tb) / 1e9,
         "frac_bf16_peak": flops / (tf + tb) / 1e9 / PEAK_BF16_TFLOPS,

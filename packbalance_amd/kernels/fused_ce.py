@@ -9,10 +9,12 @@ x's dtype and original shape and ``dw`` in W's dtype (fp32 accumulation).
 Forward: one MFMA GEMM kernel computes logits tiles in registers and keeps
 only per-token (max, sum-exp) partials and the target logit, then a combine
 kernel gives lse and the loss.  Backward streams the vocabulary in chunks
-(``vocab_chunk``: 8192 rows, or the whole vocabulary when one dlogits chunk
-of all tokens stays under ``CHUNK_BUDGET`` elements): a GEMM recomputes the
-chunk's logits and writes dlogits (bf16) directly, then two GEMMs accumulate
-dx and write the chunk's dW rows.
+(``vocab_chunk``: as many vocab rows as keep one dlogits chunk of all tokens
+under ``CHUNK_BUDGET`` elements -- 1 GiB of bf16 per layout, a small share
+of the 288 GB of HBM -- but at least 8192): a GEMM recomputes the chunk's
+logits and writes dlogits (bf16) directly, then two GEMMs accumulate dx and
+write the chunk's dW rows.  Fewer, longer chunks mean fewer passes over the
+fp32 dx accumulator (cfg4: 4 chunks of 32768 rows instead of 16 of 8192).
 Operands are bf16 with fp32 accumulation (fp32 inputs are rounded to bf16,
 as the reference's autocast GEMM does).  ``chunk_size`` (token rows per
 chunk in the reference) is accepted and validated; memory is bounded by the
@@ -76,7 +78,7 @@ def ce_rows(logits: torch.Tensor, targets: torch.Tensor, *, write_dlogits: bool,
 
 
 VOCAB_CHUNK = 8192
-CHUNK_BUDGET = 1 << 27  # dlogits elements per chunk (256 MB of bf16)
+CHUNK_BUDGET = 1 << 29  # dlogits elements per chunk (1 GiB of bf16 per layout)
 
 
 def _round8(n: int) -> int:
