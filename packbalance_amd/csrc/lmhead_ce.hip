@@ -360,22 +360,34 @@ __global__ __launch_bounds__(SH::NT) void gemm_nt_dma(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < JN; ++j) acc[i][j] = zero16();
 
+  // Fragments are double-buffered across the slice's four 16-wide K steps:
+  // step ks+1's LDS reads are in flight while step ks's MFMAs issue.
   auto compute = [&](const char *sb) {
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      bf16x8_t a[IM], b[JN];
+    bf16x8_t a[2][IM], b[2][JN];
+    auto load = [&](int ks, int buf) {
 #pragma unroll
       for (int i = 0; i < IM; ++i)
-        a[i] = *reinterpret_cast<const bf16x8_t *>(sb + aof[ks] + 4096 * i);
+        a[buf][i] = *reinterpret_cast<const bf16x8_t *>(sb + aof[ks] + 4096 * i);
 #pragma unroll
       for (int j = 0; j < JN; ++j)
-        b[j] = *reinterpret_cast<const bf16x8_t *>(sb + bof[ks] + 4096 * j);
+        b[buf][j] = *reinterpret_cast<const bf16x8_t *>(sb + bof[ks] + 4096 * j);
+    };
+    load(0, 0);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      // sched_barrier keeps the scheduler from sinking the reads back
+      // behind the MFMAs (it would reuse one fragment buffer otherwise).
+      __builtin_amdgcn_sched_barrier(0);
+      if (ks + 1 < 4) load(ks + 1, (ks + 1) & 1);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < IM; ++i)
 #pragma unroll
         for (int j = 0; j < JN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks & 1][i], b[ks & 1][j],
+                                                               acc[i][j], 0, 0, 0);
     }
+    __builtin_amdgcn_sched_barrier(0);
   };
   // One step: slice kt (in `cur`) has landed for this thread, the barrier
   // makes it visible and frees `nxt` (slice kt-1's), which takes kt+STAGES-1.
