@@ -505,20 +505,28 @@ void attn_bwd_dkdv_pipe(BwdArgs a) {
       f32x16_t sn = zero16(), pn = zero16();
       bf16x8_t pf[2], dsf[2];
       __builtin_amdgcn_sched_barrier(0);
-      // S(t+1), dP(t+1) MFMAs with the P/dS math of step t between them.
+      // S(t+1), dP(t+1) MFMAs with the P/dS math of step t between them; the
+      // dO / Q column fragments of step t (transposing reads) are spread
+      // over the same loop so they have landed when dV / dK need them.
       constexpr int JPS = 16 / NDK;  // elements per head-dim step (2 or 4)
+      constexpr int FPS = (NVF + NDK - 1) / NDK;  // column fragments per head-dim step
+      bf16x8_t gcol[NVF], qcol[NVF];
 #pragma unroll
       for (int dk = 0; dk < NDK; ++dk) {
         sn = mfma32(qa[dk], kf[dk], sn);
         pn = mfma32(ga[dk], vf[dk], pn);
 #pragma unroll
         for (int j = dk * JPS; j < (dk + 1) * JPS; j += 2) pds2(j, sc, pc, lse, dlt, pf, dsf);
+#pragma unroll
+        for (int f = dk * FPS; f < (dk + 1) * FPS && f < NVF; ++f) {
+          gcol[f] = cfrag(gslot(IR()), f);
+          qcol[f] = cfrag(qslot(IR()), f);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
       // dV(t) += P^T dO(t), dK(t) += dS^T Q(t); S(t+1) moves into sc alongside.
 #pragma unroll
-      for (int f = 0; f < NVF; ++f)
-        dvdk(f, cfrag(gslot(IR()), f), cfrag(qslot(IR()), f), pf, dsf);
+      for (int f = 0; f < NVF; ++f) dvdk(f, gcol[f], qcol[f], pf, dsf);
       sc = sn;
       pc = pn;
       if (!plan_full(e1)) mask(sc, e1, step_of(t + 1, e1).q0, dslot(IR1()));
@@ -726,8 +734,10 @@ __device__ __forceinline__ void dq_body(const BwdArgs &a) {
 // of sub-tile u, then dQ^T += K^T dS^T with K^T as column fragments of the
 // same K tile.  Head dim 64 fits two waves per SIMD (~214 registers); head
 // dim 128 needs ~320 and runs one.
+constexpr int kAheadDq = 1;  // K / V fragment reads in flight ahead of their MFMAs
+
 template <int DP, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(DP == 64 ? 2 : 1, DP == 64 ? 2 : 1)))
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_bwd_dq_pipe(BwdArgs a) {
   constexpr int NT = 64 * WAVES, BM = 32 * WAVES;
   constexpr int NDK = DP / 16, NDB = DP / 32;
@@ -921,9 +931,11 @@ void attn_bwd_dq_pipe(BwdArgs a) {
       const int e4 = entry(u + 5);
       __builtin_amdgcn_sched_barrier(0);
       dma_sub(row0(e3, u + 3), IR3());
+      // K / V row fragments of sub-tile u+1 stream kAheadDq steps ahead of
+      // their MFMAs (holding all of them costs 64 registers at D = 128).
       bf16x8_t ka[NDK], va[NDK];
 #pragma unroll
-      for (int dk = 0; dk < NDK; ++dk) {
+      for (int dk = 0; dk < kAheadDq; ++dk) {
         ka[dk] = rfrag(kslot(IR1()), dk);
         va[dk] = rfrag(vslot(IR1()), dk);
       }
@@ -933,6 +945,10 @@ void attn_bwd_dq_pipe(BwdArgs a) {
       constexpr int JPS = 16 / NDK;
 #pragma unroll
       for (int dk = 0; dk < NDK; ++dk) {
+        if (dk + kAheadDq < NDK) {
+          ka[dk + kAheadDq] = rfrag(kslot(IR1()), dk + kAheadDq);
+          va[dk + kAheadDq] = rfrag(vslot(IR1()), dk + kAheadDq);
+        }
         sn = mfma32(ka[dk], qf[dk], sn);
         pn = mfma32(va[dk], gf[dk], pn);
 #pragma unroll
