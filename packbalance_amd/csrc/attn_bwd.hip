@@ -943,6 +943,8 @@ void attn_bwd_dq_pipe(BwdArgs a) {
       bf16x8_t dsf[2];
       __builtin_amdgcn_sched_barrier(0);
       constexpr int JPS = 16 / NDK;
+      constexpr int FPS = (NVF + NDK - 1) / NDK;  // K^T fragments read per head-dim step
+      bf16x8_t kcol[NVF];
 #pragma unroll
       for (int dk = 0; dk < NDK; ++dk) {
         if (dk + kAheadDq < NDK) {
@@ -953,12 +955,14 @@ void attn_bwd_dq_pipe(BwdArgs a) {
         pn = mfma32(va[dk], gf[dk], pn);
 #pragma unroll
         for (int j = dk * JPS; j < (dk + 1) * JPS; j += 2) ds2(j, sc, pc, dsf);
+#pragma unroll
+        for (int f = dk * FPS; f < (dk + 1) * FPS && f < NVF; ++f) kcol[f] = cfrag(kslot(IR()), f);
         __builtin_amdgcn_sched_barrier(0);
       }
-      // dQ^T += K^T dS^T (A = K^T: column fragments of the K tile).
+      // dQ^T += K^T dS^T (A = K^T: column fragments of the K tile, read
+      // during the loop above).
 #pragma unroll
-      for (int f = 0; f < NVF; ++f)
-        dq_acc[f % NDB] = mfma32(cfrag(kslot(IR()), f), dsf[f / NDB], dq_acc[f % NDB]);
+      for (int f = 0; f < NVF; ++f) dq_acc[f % NDB] = mfma32(kcol[f], dsf[f / NDB], dq_acc[f % NDB]);
       sc = sn;
       pc = pn;
       if (!plan_full(e1)) mask(sc, e1, row0(e1, u + 1), dslot(IR1()));
