@@ -50,6 +50,9 @@ def _rms_case(shape, dtype, wdtype, dev, *, seed=0, row_view=False, wstd=1.0, wm
         ((64, 100), torch.float32, torch.float32),  # n not a multiple of the vector
         ((33, 8192), torch.bfloat16, torch.bfloat16),  # streaming (non-register) rows
         ((16, 96), torch.float16, torch.float32),
+        ((37, 1024), torch.float32, torch.float32),  # column-split backward, 1 vector per lane
+        ((130, 2048), torch.bfloat16, torch.float32),  # column-split, ragged last batch
+        ((9, 4096), torch.float16, torch.float16),  # column-split, 2 vectors per lane
     ],
 )
 def test_rmsnorm_matches_oracle(shape, dtype, wdtype, dev) -> None:
