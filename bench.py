@@ -476,7 +476,11 @@ def main() -> int:
         roofline = {"bound": "mfma", "kernel": f"{FWD_KERNEL} (cfg3)",
                     "achieved": a["fwd_tflops"], "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                     "frac": a["fwd_tflops"] / PEAK_BF16_TFLOPS,
-                    "traffic": counter_traffic(FWD_KERNEL)}
+                    "traffic": counter_traffic(FWD_KERNEL),
+                    "note": "the forward launch of pb_attn_fwd; the backward (pb_attn_bwd: dQ + "
+                            "dK/dV kernels, about 3/4 of attention time) runs at "
+                            f"{a['bwd_tflops'] / PEAK_BF16_TFLOPS:.3f} of peak and attention "
+                            f"fwd+bwd at {a['frac_bf16_peak']:.3f} (kernels.attention)"}
         log("kernels: fused LM-head CE (cfg4)")
         kernels["lmhead_ce"] = lmhead_ce_kernels(dev, max(2, args.kernel_iters // 3))
         log("kernels: row CE chunk")
