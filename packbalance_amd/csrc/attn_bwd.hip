@@ -256,8 +256,16 @@ struct DkdvStep {
 // documents arrive by DMA through a 4-slot ring (steps t+1 .. t+3 in flight
 // while t is computed, one barrier per step); the MFMAs of S(t+1) and
 // dP(t+1) are interleaved with the P/dS math of step t.
+// Q / dO row-fragment reads in flight ahead of their MFMAs: two at head dim
+// 64 (the registers this frees fit two waves per SIMD), all of them at 128
+// (one wave per SIMD either way; streaming them measured slower there).
+template <int DP>
+constexpr int kAheadDkdv = DP == 64 ? 2 : DP / 16;
+
+// Head dim 64 fits two waves per SIMD (with the row fragments streamed);
+// head dim 128 needs ~400 registers and runs one.
 template <int DP, int WAVES, bool SPLIT>
-__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(DP == 64 ? 2 : 1, DP == 64 ? 2 : 1)))
 void attn_bwd_dkdv_pipe(BwdArgs a) {
   constexpr int NT = 64 * WAVES, BN = 32 * WAVES;
   constexpr int NDK = DP / 16, NDB = DP / 32;
@@ -493,12 +501,13 @@ void attn_bwd_dkdv_pipe(BwdArgs a) {
       const int e4 = entry(t + 5);  // for body t + 1, issued before this body's DMA
       __builtin_amdgcn_sched_barrier(0);
       dma_step(step_of(t + 3, e3), IR3());
-      // Step t's lse/delta, step t+1's Q / dO row fragments.
+      // Step t's lse/delta; step t+1's Q / dO row fragments stream
+      // kAheadDkdv steps ahead of their MFMAs.
       float lse[16], dlt[16];
       load_ld(lslot(IR()), lse, dlt);
       bf16x8_t qa[NDK], ga[NDK];
 #pragma unroll
-      for (int dk = 0; dk < NDK; ++dk) {
+      for (int dk = 0; dk < kAheadDkdv<DP>; ++dk) {
         qa[dk] = rfrag(qslot(IR1()), dk);
         ga[dk] = rfrag(gslot(IR1()), dk);
       }
@@ -513,6 +522,10 @@ void attn_bwd_dkdv_pipe(BwdArgs a) {
       bf16x8_t gcol[NVF], qcol[NVF];
 #pragma unroll
       for (int dk = 0; dk < NDK; ++dk) {
+        if (dk + kAheadDkdv<DP> < NDK) {
+          qa[dk + kAheadDkdv<DP>] = rfrag(qslot(IR1()), dk + kAheadDkdv<DP>);
+          ga[dk + kAheadDkdv<DP>] = rfrag(gslot(IR1()), dk + kAheadDkdv<DP>);
+        }
         sn = mfma32(qa[dk], kf[dk], sn);
         pn = mfma32(ga[dk], vf[dk], pn);
 #pragma unroll
