@@ -281,27 +281,38 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs &g, f32x16_t (&acc)
   }
 }
 
-// Tile shape of one DMA-kernel instantiation.
-template <int WM_, int WN_, int IM_, int JN_, int STAGES_>
+// Tile shape of one DMA-kernel instantiation: WM x WN waves of 32*IM x 32*JN
+// outputs, K slices of KW elements (64 or 32: 128- or 64-byte LDS rows in
+// the SwzTile<KW> swizzle), a ring of STAGES slices.
+template <int WM_, int WN_, int IM_, int JN_, int STAGES_, int KW_ = 64>
 struct DmaShape {
-  static constexpr int WM = WM_, WN = WN_, IM = IM_, JN = JN_, STAGES = STAGES_;
+  static constexpr int WM = WM_, WN = WN_, IM = IM_, JN = JN_, STAGES = STAGES_, KW = KW_;
   static constexpr int NT = 64 * WM * WN, BMT = 32 * IM * WM, BNT = 32 * JN * WN;
 };
 
 template <int MODE, class SH>
 __global__ __launch_bounds__(SH::NT) void gemm_nt_dma(GemmArgs g) {
   constexpr int WM = SH::WM, WN = SH::WN, IM = SH::IM, JN = SH::JN, STAGES = SH::STAGES;
+  constexpr int KW = SH::KW, KB = 2 * KW, KS = KW / 16;  // slice width, row bytes, K steps
   constexpr int NT = SH::NT, BMT = SH::BMT, BNT = SH::BNT, W = NT / 64;
   constexpr int WR = 32 * IM, WC = 32 * JN;
-  constexpr int AB = BMT * 128, SB = AB + BNT * 128;  // bytes of one stage (A then B)
-  constexpr int NA = AB / (16 * NT), NB = BNT * 128 / (16 * NT);  // DMAs per thread per stage
-  static_assert(NA * 16 * NT == AB && NB * 16 * NT == BNT * 128, "stage / thread mismatch");
-  static_assert(STAGES == 2 || STAGES == 3, "ring of 2 or 3 slices");
+  constexpr int AB = BMT * KB, SB = AB + BNT * KB;  // bytes of one stage (A then B)
+  constexpr int NA = AB / (16 * NT), NB = BNT * KB / (16 * NT);  // DMAs per thread per stage
+  constexpr int RB32 = 32 * KB;  // bytes of 32 rows: the offset between fragment row blocks
+  static_assert(KW == 64 || KW == 32, "slice width");
+  static_assert(NA * 16 * NT == AB && NB * 16 * NT == BNT * KB, "stage / thread mismatch");
+  static_assert(STAGES >= 2 && STAGES <= 4, "ring of 2 to 4 slices");
   static_assert(MODE != kDlogits || WR * (BNT + 8) * 2 <= SB, "dlogits staging must fit a stage");
   // Stages are separate LDS objects, so the compiler does not wait for the
   // DMA into one before reading another.
-  __shared__ __align__(16) char st0[SB], st1[SB], st2[STAGES == 3 ? SB : 16];
+  __shared__ __align__(16) char st0[SB], st1[SB], st2[STAGES > 2 ? SB : 16],
+      st3[STAGES > 3 ? SB : 16];
   __shared__ float red_m[MODE == kLse ? WM : 1][BNT], red_s[MODE == kLse ? WM : 1][BNT];
+  auto slot = [&](auto Ic) -> char * {
+    constexpr int I = decltype(Ic)::value % STAGES;
+    if constexpr (I == 0) return st0; else if constexpr (I == 1) return st1;
+    else if constexpr (I == 2) return st2; else return st3;
+  };
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hh = lane >> 5, l32 = lane & 31;
@@ -312,20 +323,20 @@ __global__ __launch_bounds__(SH::NT) void gemm_nt_dma(GemmArgs g) {
   const int m0 = tm * BMT, n0 = tn * BNT;
   const int kb = MODE == kAccum && g.part ? blockIdx.y * g.k_per_split : 0;
   const int ke = MODE == kAccum && g.part ? min(g.K, kb + g.k_per_split) : g.K;
-  const int nk = (ke - kb) / 64;  // >= 1, checked by the host
+  const int nk = (ke - kb) / KW;  // >= 1, checked by the host
 
   // DMA: chunk p of a stage <- row r, 16-byte chunk c of the K-slice.
   uint32_t aoff[NA], boff[NB];
 #pragma unroll
   for (int i = 0; i < NA; ++i) {
     int r, c;
-    SwzTile<64>::at((i * W + wave) * 64 + lane, r, c);
+    SwzTile<KW>::at((i * W + wave) * 64 + lane, r, c);
     aoff[i] = (uint32_t)((r * g.lda + c * 8) * 2);
   }
 #pragma unroll
   for (int i = 0; i < NB; ++i) {
     int r, c;
-    SwzTile<64>::at((i * W + wave) * 64 + lane, r, c);
+    SwzTile<KW>::at((i * W + wave) * 64 + lane, r, c);
     boff[i] = (uint32_t)((r * g.ldb + c * 8) * 2);
   }
   const char *abase = reinterpret_cast<const char *>(g.A + (int64_t)m0 * g.lda + kb);
@@ -336,7 +347,7 @@ __global__ __launch_bounds__(SH::NT) void gemm_nt_dma(GemmArgs g) {
   // Slices past the last reload the last one into a slot nobody reads again,
   // so every step waits for the same DMA count.
   auto dma = [&](int t, char *dst) {
-    const int64_t ko = (int64_t)(t < nk ? t : nk - 1) * 128;
+    const int64_t ko = (int64_t)(t < nk ? t : nk - 1) * KB;
 #pragma unroll
     for (int i = 0; i < NA; ++i) dma16(abase + ko, alim - ko, aoff[i], dst + (i * W + wave) * 1024);
 #pragma unroll
@@ -345,13 +356,13 @@ __global__ __launch_bounds__(SH::NT) void gemm_nt_dma(GemmArgs g) {
   };
   // Fragment offsets: rows WR*wm + 32i + l32 of A, WC*wn + 32j + l32 of B,
   // 16-byte chunk 2ks + hh.  The swizzle depends on the row only through
-  // l32 (the row offsets are multiples of 16 lines), so row blocks differ by
-  // 32 rows = 4 KiB.
-  int aof[4], bof[4];
+  // l32 (the row offsets are whole multiples of the swizzle period), so row
+  // blocks differ by 32 rows.
+  int aof[KS], bof[KS];
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    aof[ks] = SwzTile<64>::off(WR * wm + l32, 16 * ks + 8 * hh);
-    bof[ks] = AB + SwzTile<64>::off(WC * wn + l32, 16 * ks + 8 * hh);
+  for (int ks = 0; ks < KS; ++ks) {
+    aof[ks] = SwzTile<KW>::off(WR * wm + l32, 16 * ks + 8 * hh);
+    bof[ks] = AB + SwzTile<KW>::off(WC * wn + l32, 16 * ks + 8 * hh);
   }
 
   f32x16_t acc[IM][JN];
@@ -360,25 +371,25 @@ __global__ __launch_bounds__(SH::NT) void gemm_nt_dma(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < JN; ++j) acc[i][j] = zero16();
 
-  // Fragments are double-buffered across the slice's four 16-wide K steps:
-  // step ks+1's LDS reads are in flight while step ks's MFMAs issue.
+  // Fragments are double-buffered across the slice's K steps: step ks+1's
+  // LDS reads are in flight while step ks's MFMAs issue.
   auto compute = [&](const char *sb) {
     bf16x8_t a[2][IM], b[2][JN];
     auto load = [&](int ks, int buf) {
 #pragma unroll
       for (int i = 0; i < IM; ++i)
-        a[buf][i] = *reinterpret_cast<const bf16x8_t *>(sb + aof[ks] + 4096 * i);
+        a[buf][i] = *reinterpret_cast<const bf16x8_t *>(sb + aof[ks] + RB32 * i);
 #pragma unroll
       for (int j = 0; j < JN; ++j)
-        b[buf][j] = *reinterpret_cast<const bf16x8_t *>(sb + bof[ks] + 4096 * j);
+        b[buf][j] = *reinterpret_cast<const bf16x8_t *>(sb + bof[ks] + RB32 * j);
     };
     load(0, 0);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+    for (int ks = 0; ks < KS; ++ks) {
       // sched_barrier keeps the scheduler from sinking the reads back
       // behind the MFMAs (it would reuse one fragment buffer otherwise).
       __builtin_amdgcn_sched_barrier(0);
-      if (ks + 1 < 4) load(ks + 1, (ks + 1) & 1);
+      if (ks + 1 < KS) load(ks + 1, (ks + 1) & 1);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < IM; ++i)
@@ -389,33 +400,35 @@ __global__ __launch_bounds__(SH::NT) void gemm_nt_dma(GemmArgs g) {
     }
     __builtin_amdgcn_sched_barrier(0);
   };
-  // One step: slice kt (in `cur`) has landed for this thread, the barrier
-  // makes it visible and frees `nxt` (slice kt-1's), which takes kt+STAGES-1.
-  auto step = [&](int kt, const char *cur, char *nxt) {
+  // One step: slice kt (in slot kt % STAGES) has landed for this thread, the
+  // barrier makes it visible and frees slot (kt - 1) % STAGES, which takes
+  // slice kt + STAGES - 1.
+  auto step = [&](int kt, auto Ic) {
+    constexpr int I = decltype(Ic)::value;
     wait_vmcnt<(STAGES - 2) * (NA + NB)>();
     block_sync_nofence();
-    dma(kt + STAGES - 1, nxt);
-    compute(cur);
+    dma(kt + STAGES - 1, slot(std::integral_constant<int, I + STAGES - 1>()));
+    compute(slot(Ic));
   };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  dma(0, st0);
+  if constexpr (STAGES > 2) dma(1, st1);
+  if constexpr (STAGES > 3) dma(2, st2);
   int kt = 0;
-  if constexpr (STAGES == 3) {
-    dma(0, st0);
-    dma(1, st1);
-    for (; kt + 3 <= nk; kt += 3) {
-      step(kt, st0, st2);
-      step(kt + 1, st1, st0);
-      step(kt + 2, st2, st1);
-    }
-    if (kt < nk) step(kt, st0, st2);
-    if (kt + 1 < nk) step(kt + 1, st1, st0);
-  } else {
-    dma(0, st0);
-    for (; kt + 2 <= nk; kt += 2) {
-      step(kt, st0, st1);
-      step(kt + 1, st1, st0);
-    }
-    if (kt < nk) step(kt, st0, st1);
+  for (; kt + STAGES <= nk; kt += STAGES) {
+    step(kt, I0());
+    step(kt + 1, I1());
+    if constexpr (STAGES > 2) step(kt + 2, I2());
+    if constexpr (STAGES > 3) step(kt + 3, I3());
   }
+  if (kt < nk) step(kt, I0());
+  if constexpr (STAGES > 2)
+    if (kt + 1 < nk) step(kt + 1, I1());
+  if constexpr (STAGES > 3)
+    if (kt + 2 < nk) step(kt + 2, I2());
   wait_vmcnt<0>();
   __syncthreads();  // every wave is done with the stages (kDlogits stages in st0)
   gemm_epilogue<MODE, WM, WN, IM, JN>(g, acc, tm, m0, n0, reinterpret_cast<bf16_t *>(st0), red_m,
@@ -606,12 +619,23 @@ unsigned tiles(int m, int n) { return (unsigned)(((m + BM - 1) / BM) * ((n + BN 
 // three-slice ring of 48 KiB slices.  Smaller tiles need more bytes per flop
 // and a 2-slice ring does not cover the operand latency (measured slower).
 using RowShape = DmaShape<4, 2, 2, 2, 3>;
+// 256 x 256 tiles on 8 waves of 128 x 64 (6 fragment reads per 8 MFMAs
+// instead of 4 per 4, half the operand bytes per flop), 32-wide K slices in
+// a four-slice ring of 32 KiB.  Used for the forward (lse) product when the
+// grid still has >= 1024 tiles (four per CU): cfg4 16.1 -> 15.6 ms.  The
+// backward products measured slower on it (dx and dW 51.8 -> 52.8 ms for
+// the chunk loop), and dlogits' staging takes 128 tokens, so they keep
+// RowShape.
+using WideShape = DmaShape<2, 4, 4, 2, 4, 32>;
 template <class SH> unsigned dma_tiles(int m, int n) {
   return (unsigned)(((m + SH::BMT - 1) / SH::BMT) * ((n + SH::BNT - 1) / SH::BNT));
 }
 // The DMA kernel takes K-slices of whole 64-element blocks (operands are
 // already 16-byte aligned with row strides % 8 == 0).
 bool dma_ok(int64_t k) { return k > 0 && k % 64 == 0; }
+bool wide_ok(int64_t m, int64_t n, int64_t k) {
+  return dma_ok(k) && dma_tiles<WideShape>((int)m, (int)n) >= 1024;
+}
 
 }  // namespace ce
 }  // namespace pb
@@ -684,8 +708,8 @@ extern "C" int pb_lmhead_ce_fwd(const void *x, int64_t ldx, const void *w, int64
     hipLaunchKernelGGL(sum_rows, dim3(1), dim3(1024), 0, st, (const float *)nullptr, 0, loss_sum);
     return launch_status("pb_lmhead_ce_fwd(empty)");
   }
-  const bool dma = dma_ok(d);
-  const int bm = dma ? RowShape::BMT : BM;  // vocab rows per tile = lse partials per token
+  const bool dma = dma_ok(d), wide = wide_ok(v, n, d);
+  const int bm = wide ? WideShape::BMT : dma ? RowShape::BMT : BM;  // lse partials per token
   const int nmt = (int)((v + bm - 1) / bm);
   float *ws = static_cast<float *>(workspace);
   GemmArgs g = {};
@@ -701,7 +725,10 @@ extern "C" int pb_lmhead_ce_fwd(const void *x, int64_t ldx, const void *w, int64
   g.part_m = ws;
   g.part_s = ws + (int64_t)nmt * n;
   g.tgt = ws + 2 * (int64_t)nmt * n;
-  if (dma)
+  if (wide)
+    hipLaunchKernelGGL((gemm_nt_dma<kLse, WideShape>), dim3(dma_tiles<WideShape>(g.M, g.N)),
+                       dim3(WideShape::NT), 0, st, g);
+  else if (dma)
     hipLaunchKernelGGL((gemm_nt_dma<kLse, RowShape>), dim3(dma_tiles<RowShape>(g.M, g.N)),
                        dim3(RowShape::NT), 0, st, g);
   else
