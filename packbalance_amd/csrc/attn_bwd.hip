@@ -749,8 +749,11 @@ __device__ __forceinline__ void dq_body(const BwdArgs &a) {
 // dim 128 needs ~320 and runs one.
 constexpr int kAheadDq = 1;  // K / V fragment reads in flight ahead of their MFMAs
 
+// Two waves per SIMD where the registers allow it (D = 64, and D = 128 with
+// 4-wave workgroups); the 2-wave D = 128 variant needs more and runs one.
 template <int DP, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(64 * WAVES)
+__attribute__((amdgpu_waves_per_eu(DP == 64 || WAVES == 4 ? 2 : 1, DP == 64 || WAVES == 4 ? 2 : 1)))
 void attn_bwd_dq_pipe(BwdArgs a) {
   constexpr int NT = 64 * WAVES, BM = 32 * WAVES;
   constexpr int NDK = DP / 16, NDB = DP / 32;

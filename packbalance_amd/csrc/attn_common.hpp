@@ -258,14 +258,16 @@ inline AttnConfig attn_config(int64_t b, int64_t hq, int64_t hkv, int64_t s, int
   c.dq_waves = big_q ? 4 : 2;
   c.kv_waves = b * hkv * tiles(128) >= kFill ? 4 : 2;
   c.split = (c.kv_waves == 2 && b * hkv * tiles(64) < kFill && hq > hkv) ? 1 : 0;
-  // Aim for ~4096 chunk workgroups over all lists, but at least 4 KV tiles
-  // each (a chunk also pays the prologue and the merge).
+  // Aim for ~2048 chunk workgroups over all lists, but at least 4 KV tiles
+  // each (a chunk also pays the prologue and the merge).  Measured on the
+  // cfg2 step (two [2, 2048] micro-batches on two streams; attention kernel
+  // time per 9 traced steps): ~4096 chunks 30.6 ms, ~2048 29.4, no split 29.6.
   auto kv_split = [&](int64_t q_rows, int &chunk_out, int &splits_out) {
     chunk_out = 0;
     splits_out = 1;
     const int64_t base = b * hq * tiles((int)q_rows), nkt = tiles(64);
     if (base >= 4 * kFill) return;
-    int64_t chunk = (nkt * base + 4095) / 4096;
+    int64_t chunk = (nkt * base + 2047) / 2048;
     if (chunk < 4) chunk = 4;
     if (chunk < nkt) {
       chunk_out = (int)chunk;
