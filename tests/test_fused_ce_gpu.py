@@ -75,6 +75,7 @@ def test_reference_gpu_case(dev) -> None:
         ((4, 50), 517, 40, torch.float32, torch.float32, 0.0),  # d % 8 != 0, v odd
         ((2048,), 32000, 768, torch.float32, torch.float32, 0.0),  # cfg2 dtype flow
         ((192,), 4160, 128, torch.bfloat16, torch.bfloat16, 0.01),  # DMA GEMMs, ragged tiles
+        ((1030,), 66000, 64, torch.bfloat16, torch.bfloat16, 0.0),  # 256x256 lse tiles, ragged
     ],
 )
 def test_fused_ce_matches_oracle(shape, v, d, xdt, wdt, z, dev) -> None:
