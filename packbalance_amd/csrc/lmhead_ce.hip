@@ -6,12 +6,14 @@
 // gradients dlogits = softmax*(1 + 2z*lse) - onehot (fused_ce.py:80-84),
 // dx = dlogits W, dW = dlogits^T x, both scaled by grad_output.
 //
-// Everything runs on one bf16 MFMA GEMM tile, C[m][n] = sum_k A[m][k] B[n][k]
-// (both operands K-contiguous, "NT"), 128 x 128 x 64 per workgroup, four waves
-// of 64 x 64 (2 x 2 v_mfma_f32_32x32x16_bf16 blocks), register-prefetched
-// double buffering through LDS.  Four epilogues:
+// Everything runs on one bf16 MFMA GEMM, C[m][n] = sum_k A[m][k] B[n][k]
+// (both operands K-contiguous, "NT"), with four epilogues.  gemm_nt_dma takes
+// K in whole 64-element slices: LDS-DMA rings of swizzled slices, 256 x 128
+// tiles on 8 waves for the backward products and 256 x 256 tiles for the
+// forward; gemm_nt (128 x 128 x 64, four waves of 64 x 64, register-staged)
+// handles any other K.  Epilogues:
 //   kLse      A = W, B = x: C = logits^T, lane <-> token.  Per token, a
-//             (max, sum exp) partial over the tile's 128 vocab rows and the
+//             (max, sum exp) partial over the tile's vocab rows and the
 //             target logit; the [tokens x vocab] tile is discarded.
 //   kDlogits  same product over one vocab chunk; writes dlogits (scaled by the
 //             device-resident grad_output) as dL [tokens][chunk] and dL^T.
