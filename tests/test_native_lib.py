@@ -51,3 +51,23 @@ def test_workspace_query_is_host_only() -> None:
     lib = N.lib()
     assert lib.pb_rmsnorm_bwd_workspace_bytes(0, 16) == 0
     assert lib.pb_rmsnorm_bwd_workspace_bytes(32768, 4096) > 0
+
+
+def test_ce_rows_dl_rejects_bad_dtype_on_host() -> None:
+    lib = N.lib()
+    rc = lib.pb_ce_rows_dl(None, 8, 1, N.PB_F32, None, None, None, None, 8, 1, 99, 1, 8, -100,
+                           0.0, None)
+    assert rc == N.PB_EINVAL
+    assert b"dlogits dtype" in lib.pb_last_error()
+
+
+def test_vocab_chunk_budget() -> None:
+    from packbalance_amd.kernels.fused_ce import CHUNK_BUDGET, VOCAB_CHUNK, vocab_chunk
+
+    assert vocab_chunk(16384, 128256) == 32768  # cfg4: 4 chunks of dlogits
+    assert vocab_chunk(4096, 32000) == 32000  # a cfg2 micro-batch: the whole vocabulary
+    for n, v in [(1, 7), (129, 8200), (16384, 128256), (10**6, 50000), (37, 100003)]:
+        c = vocab_chunk(n, v)
+        v8 = (v + 7) // 8 * 8
+        assert c % 8 == 0 and min(VOCAB_CHUNK, v8) <= c <= v8
+        assert n * c <= max(CHUNK_BUDGET, n * VOCAB_CHUNK)
