@@ -76,6 +76,7 @@ def test_reference_gpu_case(dev) -> None:
         ((2048,), 32000, 768, torch.float32, torch.float32, 0.0),  # cfg2 dtype flow
         ((192,), 4160, 128, torch.bfloat16, torch.bfloat16, 0.01),  # DMA GEMMs, ragged tiles
         ((1030,), 66000, 64, torch.bfloat16, torch.bfloat16, 0.0),  # 256x256 lse tiles, ragged
+        ((3,), 5000, 64, torch.bfloat16, torch.bfloat16, 0.01),  # DMA tiles almost all past N
     ],
 )
 def test_fused_ce_matches_oracle(shape, v, d, xdt, wdt, z, dev) -> None:
