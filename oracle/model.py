@@ -69,25 +69,41 @@ def _chunked_ce(x, w, targets, chunk_size, z):
     return total
 
 
+def _attention(x, p, pre, cfg, position_ids, doc_ids):
+    # llama.py:77-103: q/k/v projections, RoPE on q and k, document-masked
+    # attention, heads back to [B, S, Hq * D], then o_proj.
+    b, s, _ = x.shape
+    hd = cfg.d_model // cfg.n_heads
+    q = (x @ p[pre + "self_attn.q_proj.weight"].t()).view(b, s, cfg.n_heads, hd).transpose(1, 2)
+    k = (x @ p[pre + "self_attn.k_proj.weight"].t()).view(b, s, cfg.n_kv_heads, hd).transpose(1, 2)
+    v = (x @ p[pre + "self_attn.v_proj.weight"].t()).view(b, s, cfg.n_kv_heads, hd).transpose(1, 2)
+    q, k = _rope(q, k, position_ids, hd, cfg.rope_theta)
+    a = _eager_attention(q, k, v, doc_ids)
+    return a.transpose(1, 2).reshape(b, s, -1) @ p[pre + "self_attn.o_proj.weight"].t()
+
+
+def _mlp(x, p, pre):
+    # llama.py:57-61: silu(gate_proj(x)) * up_proj(x), then down_proj.
+    gate = x @ p[pre + "mlp.gate_proj.weight"].t()
+    up = x @ p[pre + "mlp.up_proj.weight"].t()
+    return (F.silu(gate) * up) @ p[pre + "mlp.down_proj.weight"].t()
+
+
+def _layer(h, p, pre, cfg, position_ids, doc_ids):
+    # llama.py:122-125: pre-norm residual blocks; the residual stream h is
+    # carried un-normalised and each block's output is added to it.
+    eps = cfg.norm_eps
+    h = h + _attention(_rmsnorm(h, p[pre + "input_layernorm.weight"], eps), p, pre, cfg,
+                       position_ids, doc_ids)
+    return h + _mlp(_rmsnorm(h, p[pre + "post_attention_layernorm.weight"], eps), p, pre)
+
+
 def loss(params: dict[str, torch.Tensor], cfg, input_ids, labels, position_ids, doc_ids):
     """Summed CE loss of one pack batch through the eager CPU path (differentiable)."""
     p = params
-    hd = cfg.d_model // cfg.n_heads
-    b, s = input_ids.shape
     h = F.embedding(input_ids, p["embed_tokens.weight"])
     for i in range(cfg.n_layers):
-        pre = f"layers.{i}."
-        x = _rmsnorm(h, p[pre + "input_layernorm.weight"], cfg.norm_eps)
-        q = (x @ p[pre + "self_attn.q_proj.weight"].t()).view(b, s, cfg.n_heads, hd).transpose(1, 2)
-        k = (x @ p[pre + "self_attn.k_proj.weight"].t()).view(b, s, cfg.n_kv_heads, hd).transpose(1, 2)
-        v = (x @ p[pre + "self_attn.v_proj.weight"].t()).view(b, s, cfg.n_kv_heads, hd).transpose(1, 2)
-        q, k = _rope(q, k, position_ids, hd, cfg.rope_theta)
-        a = _eager_attention(q, k, v, doc_ids)
-        h = h + a.transpose(1, 2).reshape(b, s, -1) @ p[pre + "self_attn.o_proj.weight"].t()
-        x = _rmsnorm(h, p[pre + "post_attention_layernorm.weight"], cfg.norm_eps)
-        gate = x @ p[pre + "mlp.gate_proj.weight"].t()
-        up = x @ p[pre + "mlp.up_proj.weight"].t()
-        h = h + (F.silu(gate) * up) @ p[pre + "mlp.down_proj.weight"].t()
+        h = _layer(h, p, f"layers.{i}.", cfg, position_ids, doc_ids)
     h = _rmsnorm(h, p["norm.weight"], cfg.norm_eps)
     return _chunked_ce(h, p["embed_tokens.weight"], labels, cfg.ce_chunk_size, cfg.z_loss_coeff)
 

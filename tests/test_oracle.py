@@ -556,3 +556,144 @@ def test_model_oracle_pins_catch_planted_mistakes(monkeypatch) -> None:
                       q, k.repeat_interleave(q.shape[1] // k.shape[1], 1),
                       v.repeat_interleave(q.shape[1] // k.shape[1], 1), is_causal=True))
         assert differs()
+
+
+# ---------------------------------------------------------------- model composition
+def _np_rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    return x / np.sqrt((x * x).mean(-1, keepdims=True) + eps) * w
+
+
+def _np_ce_sum(h: np.ndarray, emb: np.ndarray, labels: np.ndarray) -> float:
+    """Sum over labelled rows of logsumexp(h E^T) - (h E^T)[label], by hand."""
+    z = h @ emb.T
+    m = z.max(-1, keepdims=True)
+    lse = (m + np.log(np.exp(z - m).sum(-1, keepdims=True)))[:, 0]
+    rows = np.nonzero(labels != -100)[0]
+    return float(sum(lse[t] - z[t, labels[t]] for t in rows))
+
+
+def _one_layer(seed: int):
+    cfg, params = _tiny_model(seed=seed)
+    cfg.n_layers = 1
+    params = {n: t for n, t in params.items() if not n.startswith("layers.1.")}
+    # Logits ~4x larger than at init, so the summed CE resolves the direction
+    # of the final hidden state (a composition mistake moves it by ~1e-2).
+    with torch.no_grad():
+        params["norm.weight"].mul_(4.0)
+    return cfg, params
+
+
+def _composition_case():
+    g = torch.Generator().manual_seed(11)
+    docs = [torch.randint(0, 37, (n,), generator=g) for n in (5, 1, 8)]
+    return _pack(docs, 16)
+
+
+def _attention_closed_form_error(loss_fn) -> float:
+    """Relative loss error of `loss_fn` on a 1-layer model whose q/k projections
+    are zero and whose MLP output is zero (down_proj = 0).
+
+    Zero scores make each query's softmax uniform over its document's causal
+    prefix, so head h's output at position t is the mean of the value rows
+    (KV head h // G) over the positions tau <= t of t's document, and zero on
+    pad rows.  With pre-norm residual blocks (llama.py:122-125):
+        h1 = E[ids] + concat_h(prefix mean of v_h) Wo^T,  v = rmsnorm(E[ids]; w1) Wv^T
+    then the final norm and the tied LM head give the summed CE."""
+    cfg, params = _one_layer(seed=21)
+    with torch.no_grad():
+        for n in ("q_proj", "k_proj"):
+            params[f"layers.0.self_attn.{n}.weight"].zero_()
+        params["layers.0.mlp.down_proj.weight"].zero_()
+    ids, lab, pos, doc = _composition_case()
+    P = {n: t.detach().numpy() for n, t in params.items()}
+    eps, hd, G = cfg.norm_eps, cfg.d_model // cfg.n_heads, cfg.n_heads // cfg.n_kv_heads
+    h0 = P["embed_tokens.weight"][ids[0].numpy()]
+    v = _np_rmsnorm(h0, P["layers.0.input_layernorm.weight"], eps) @ P["layers.0.self_attn.v_proj.weight"].T
+    d = doc[0].numpy()
+    S = h0.shape[0]
+    a = np.zeros((S, cfg.n_heads * hd))
+    for t in range(S):
+        if d[t] < 0:
+            continue
+        prefix = [tau for tau in range(t + 1) if d[tau] == d[t]]
+        for h in range(cfg.n_heads):
+            kvh = h // G
+            a[t, h * hd:(h + 1) * hd] = v[prefix, kvh * hd:(kvh + 1) * hd].mean(0)
+    h1 = h0 + a @ P["layers.0.self_attn.o_proj.weight"].T
+    hf = _np_rmsnorm(h1, P["norm.weight"], eps)
+    want = _np_ce_sum(hf, P["embed_tokens.weight"], lab[0].numpy())
+    got = float(loss_fn(params, cfg, ids, lab, pos, doc).detach())
+    return abs(got - want) / abs(want)
+
+
+def _mlp_closed_form_error(loss_fn) -> float:
+    """Relative loss error of `loss_fn` on a 1-layer model whose attention
+    output is zero (v_proj = 0) and whose gate projection is twice its up
+    projection.  Then gate = 2u with u = rmsnorm(E[ids]; w2) Wu^T, and
+    silu(gate) * up = 2u * sigmoid(2u) * u, so
+        h2 = E[ids] + (2 u^2 sigmoid(2u)) Wd^T
+    (swapping the roles of gate and up would give 2 u^2 sigmoid(u))."""
+    cfg, params = _one_layer(seed=22)
+    with torch.no_grad():
+        params["layers.0.self_attn.v_proj.weight"].zero_()
+        params["layers.0.mlp.gate_proj.weight"].copy_(2.0 * params["layers.0.mlp.up_proj.weight"])
+    ids, lab, pos, doc = _composition_case()
+    P = {n: t.detach().numpy() for n, t in params.items()}
+    eps = cfg.norm_eps
+    h0 = P["embed_tokens.weight"][ids[0].numpy()]
+    u = _np_rmsnorm(h0, P["layers.0.post_attention_layernorm.weight"], eps) @ P["layers.0.mlp.up_proj.weight"].T
+    act = 2.0 * u * u / (1.0 + np.exp(-2.0 * u))
+    h2 = h0 + act @ P["layers.0.mlp.down_proj.weight"].T
+    hf = _np_rmsnorm(h2, P["norm.weight"], eps)
+    want = _np_ce_sum(hf, P["embed_tokens.weight"], lab[0].numpy())
+    got = float(loss_fn(params, cfg, ids, lab, pos, doc).detach())
+    return abs(got - want) / abs(want)
+
+
+# oracle/model.py computes RMSNorm in fp32 (reference.py:10 takes x.float()).
+_COMPOSITION_TOL = 2e-6
+
+
+def test_model_oracle_composition_closed_forms() -> None:
+    """oracle/model.py's layer composition against two hand-computed closed forms:
+    uniform attention (zero q/k projections) through o_proj into the residual
+    stream, and a SwiGLU whose gate is twice its up projection."""
+    from oracle import model as OM
+
+    assert _attention_closed_form_error(OM.loss) < _COMPOSITION_TOL
+    assert _mlp_closed_form_error(OM.loss) < _COMPOSITION_TOL
+
+
+def test_model_oracle_composition_catches_planted_mistakes(monkeypatch) -> None:
+    """Each of three composition mistakes planted in the oracle moves one of the
+    closed forms far outside its tolerance: gate and up swapped (llama.py:57-61),
+    the residual taken after the norm, and o_proj skipped (llama.py:102-103,
+    122-125)."""
+    from oracle import model as OM
+
+    def swapped_mlp(x, p, pre):
+        gate = x @ p[pre + "mlp.gate_proj.weight"].t()
+        up = x @ p[pre + "mlp.up_proj.weight"].t()
+        return (F.silu(up) * gate) @ p[pre + "mlp.down_proj.weight"].t()
+
+    def post_norm_residual(h, p, pre, cfg, position_ids, doc_ids):
+        eps = cfg.norm_eps
+        x = OM._rmsnorm(h, p[pre + "input_layernorm.weight"], eps)
+        h = x + OM._attention(x, p, pre, cfg, position_ids, doc_ids)
+        x = OM._rmsnorm(h, p[pre + "post_attention_layernorm.weight"], eps)
+        return x + OM._mlp(x, p, pre)
+
+    real_attention = OM._attention
+
+    def no_o_proj(x, p, pre, cfg, position_ids, doc_ids):
+        q = dict(p)
+        q[pre + "self_attn.o_proj.weight"] = torch.eye(cfg.d_model, dtype=x.dtype)
+        return real_attention(x, q, pre, cfg, position_ids, doc_ids)
+
+    for name, fn, check in (("_mlp", swapped_mlp, _mlp_closed_form_error),
+                            ("_layer", post_norm_residual, _attention_closed_form_error),
+                            ("_attention", no_o_proj, _attention_closed_form_error)):
+        with monkeypatch.context() as m:
+            m.setattr(OM, name, fn)
+            err = check(OM.loss)
+        assert err > 100 * _COMPOSITION_TOL, (name, err)
