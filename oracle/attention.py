@@ -30,13 +30,19 @@ def _chunk_rows(heads: int, keys: int, budget_bytes: int = 1 << 27) -> int:
 
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, doc_ids: torch.Tensor,
               dout: torch.Tensor | None = None, *, semantics: str = "flex",
-              scale: float | None = None, dtype: torch.dtype = torch.float64):
+              scale: float | None = None, dtype: torch.dtype = torch.float64,
+              delta_out: torch.Tensor | None = None):
     """Document-masked causal GQA attention in float64.
 
     q [B, Hq, S, D], k/v [B, Hkv, S, D], doc_ids [B, S] (int), dout like q.
     semantics: "flex"  -> mask_mod of attention.py:43-44 (pads attend to pads);
                "eager" -> eager_attention of attention.py:66-95 (pad rows are 0
                           and never attend or get attended).
+    delta_out: the output whose rowsum(dO * O) enters dS (default: the exact
+               O computed here).  A backward reads its forward's STORED output,
+               so passing a bf16 output models what any bf16-output
+               implementation computes (FlexAttention's backward included:
+               its delta is rowsum(dO * OUT) of the stored OUT).
     Returns dict with out [B,Hq,S,D], lse [B,Hq,S] (natural log; -inf on rows
     with no allowed key) and, if dout is given, dq, dk, dv (CPU, ``dtype``;
     float64 unless a caller trades precision for speed on large packs).
@@ -54,6 +60,7 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, doc_ids: torch.
     K = k.detach().to(dev, dtype).repeat_interleave(G, dim=1)
     V = v.detach().to(dev, dtype).repeat_interleave(G, dim=1)
     dO = None if dout is None else dout.detach().to(dev, dtype)
+    Od = None if delta_out is None else delta_out.detach().to(dev, dtype)
     docs = doc_ids.detach().to(dev, torch.int64).reshape(B, S)
 
     out = torch.zeros(B, Hq, S, D, dtype=dtype)
@@ -95,7 +102,8 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, doc_ids: torch.
             if dO is not None:
                 do = dO[b, :, r0:r1]
                 dp = torch.einsum("hqd,hkd->hqk", do, V[b, :, lo:r1])
-                delta = (do * o).sum(dim=-1, keepdim=True)
+                od = o if Od is None else Od[b, :, r0:r1]
+                delta = (do * od).sum(dim=-1, keepdim=True)
                 ds = p * (dp - delta)
                 dq[b, :, r0:r1] = torch.einsum("hqk,hkd->hqd", ds, K[b, :, lo:r1]) * sc
                 dk_full[b, :, lo:r1] += torch.einsum("hqk,hqd->hkd", ds, Q[b, :, r0:r1]) * sc
@@ -105,6 +113,49 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, doc_ids: torch.
         res["dq"] = dq
         res["dk"] = dk_full.reshape(B, Hkv, G, S, D).sum(dim=2)
         res["dv"] = dv_full.reshape(B, Hkv, G, S, D).sum(dim=2)
+    return res
+
+
+def attention_rows(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, doc_ids: torch.Tensor,
+                   dout: torch.Tensor, rows: list[torch.Tensor], *,
+                   dtype: torch.dtype = torch.float64) -> dict[str, list[torch.Tensor]]:
+    """``attention`` (flex semantics, default scale) at chosen query rows only.
+
+    rows[b] = query positions of pack b.  Out, lse and dQ of a query row depend
+    only on that row (its keys are the same-document positions <= it), so
+    they are computed row by row, with no S x S work: out[b] [Hq, n, D],
+    lse[b] [Hq, n], dq[b] [Hq, n, D] for the n rows of pack b, in ``dtype``.
+    """
+    B, Hq, S, D = q.shape
+    Hkv = k.shape[1]
+    G = Hq // Hkv
+    sc = 1.0 / math.sqrt(D)
+    docs = doc_ids.detach().to("cpu", torch.int64).reshape(B, S)
+    res: dict[str, list[torch.Tensor]] = {"out": [], "lse": [], "dq": []}
+    for b in range(B):
+        r = rows[b].to(torch.int64)
+        # query head h = c * G + g reads KV head c
+        Q = q[b].detach()[:, r.to(q.device)].to("cpu", dtype).view(Hkv, G, len(r), D)
+        dO = dout[b].detach()[:, r.to(q.device)].to("cpu", dtype).view(Hkv, G, len(r), D)
+        K = k[b].detach().to("cpu", dtype)
+        V = v[b].detach().to("cpu", dtype)
+        out = torch.zeros(Hkv, G, len(r), D, dtype=dtype)
+        lse = torch.full((Hkv, G, len(r)), -math.inf, dtype=dtype)
+        dq = torch.zeros_like(out)
+        for n, qi in enumerate(r.tolist()):
+            keys = torch.nonzero(docs[b, : qi + 1] == docs[b, qi]).flatten()
+            Kk, Vk = K[:, keys], V[:, keys]
+            s = torch.einsum("cgd,ckd->cgk", Q[:, :, n], Kk) * sc
+            lse[:, :, n] = torch.logsumexp(s, dim=-1)
+            p = torch.exp(s - lse[:, :, n, None])
+            o = torch.einsum("cgk,ckd->cgd", p, Vk)
+            out[:, :, n] = o
+            dp = torch.einsum("cgd,ckd->cgk", dO[:, :, n], Vk)
+            ds = p * (dp - (dO[:, :, n] * o).sum(-1, keepdim=True))
+            dq[:, :, n] = torch.einsum("cgk,ckd->cgd", ds, Kk) * sc
+        res["out"].append(out.reshape(Hq, len(r), D))
+        res["lse"].append(lse.reshape(Hq, len(r)))
+        res["dq"].append(dq.reshape(Hq, len(r), D))
     return res
 
 

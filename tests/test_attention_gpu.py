@@ -93,10 +93,15 @@ def test_reference_flex_test_case(dev) -> None:
         (1, 4, 2, 130, 100, [64, 66]),  # split dK/dV, element-wise reduce (D % 8 != 0)
         (1, 8, 2, 1024, 128, [300, 1, 400, -323]),  # pipelined path, 32 query rows per wave
         (2, 16, 4, 2048, 64, "cfg2"),  # pipelined path, 64 query rows per wave, D 64
-        # head-split dK/dV with KV lists of >= 32 steps walked as two halves:
+        # head-split dK/dV with KV lists of >= 16 steps (kKvChunkSteps) walked
+        # as two halves:
         (1, 12, 4, 2048, 64, [2048]),  # one dense document (64-step lists)
         (1, 8, 2, 2048, 128, [1100, -948]),  # D 128, a long document then padding
         (2, 6, 2, 1536, 64, [1000, 536]),  # two packs, both documents over the threshold
+        # the threshold itself: the 512-token document's first KV tile has a
+        # 16-step list (two halves), every other tile 14 steps or fewer (whole)
+        (1, 8, 2, 1024, 64, [512, 448, -64]),
+        (1, 8, 2, 1024, 128, [512, 448, -64]),
     ],
 )
 def test_attention_matches_oracle(B, Hq, Hkv, S, D, docs, dev) -> None:
@@ -124,6 +129,11 @@ def test_attention_contiguous_layout_and_scale(dev) -> None:
     out, dq, dk, dv = _run(q, k, v, do, doc, scale=0.3)
     ref = OA.attention(q, k, v, doc.cpu(), do, scale=0.3)
     _close(out, ref["out"], "out")
+    # The north star's 2e-2 bar, against the oracle whose delta is formed
+    # from the stored bf16 output (as the reference's own backward forms it).
+    stored = OA.attention(q, k, v, doc.cpu(), do, scale=0.3, delta_out=out.detach().cpu())
+    for got, name in ((dq, "dq"), (dk, "dk"), (dv, "dv")):
+        _close(got, stored[name], f"{name} (delta from the stored output)")
     gtol = TOL * 0.3 * math.sqrt(64)
     for got, name in ((dq, "dq"), (dk, "dk"), (dv, "dv")):
         torch.testing.assert_close(got.detach().float().cpu(), ref[name].float(), atol=gtol,
@@ -195,6 +205,29 @@ def test_attention_cfg3_pack(pack, dev) -> None:
     assert torch.isfinite(out.float()).all() and torch.isfinite(dq.float()).all()
 
 
+def test_attention_cfg3_sampled_rows_all_packs(dev) -> None:
+    """cfg3 shape, every pack and every query head (all 8 KV groups): out and dQ
+    at 24 sampled query rows per pack -- each document's first and last row,
+    the pack's last row and random ones -- against the float64 row oracle."""
+    packs = W.cfg3_packs()
+    S, Hq, Hkv, D = 8192, 32, 8, 128
+    doc = W.doc_ids_from_lengths(packs, S).to(dev)
+    q, k, v, do = _inputs(8, Hq, Hkv, S, D, dev, seed=4)
+    out, dq, _, _ = _run(q, k, v, do, doc)
+    g = torch.Generator().manual_seed(12)
+    rows = []
+    for lens in packs:
+        starts = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)[:-1]))
+        ends = torch.tensor(lens).cumsum(0) - 1
+        pick = torch.cat([starts[:4], ends[:4], torch.tensor([S - 1]),
+                          torch.randint(0, S, (15,), generator=g)])
+        rows.append(pick.unique())
+    ref = OA.attention_rows(q, k, v, doc.cpu(), do, rows)
+    for b in range(8):
+        _close(out[b][:, rows[b]], ref["out"][b], f"pack {b} out")
+        _close(dq[b][:, rows[b]], ref["dq"][b], f"pack {b} dq")
+
+
 @pytest.mark.parametrize("layout", ["mixed", "noncontiguous"])
 def test_attention_large_grid_layouts(layout, dev) -> None:
     """A large-grid D 128 shape (>= 2048 query tiles per launch, no KV split) with
@@ -244,6 +277,11 @@ def test_attention_running_max_moves(profile, D, dev) -> None:
     _close(out, ref["out"], f"{what} out")
     _close(dk, ref["dk"], f"{what} dk")
     _close(dv, ref["dv"], f"{what} dv")
+    # The north star's 2e-2 bar for dQ, against the oracle whose delta is
+    # formed from the stored bf16 output (as the reference's own backward
+    # forms it), so the bf16 rounding of O is on both sides.
+    stored = OA.attention(q, k, v, doc.cpu(), do, delta_out=out.detach().cpu())
+    _close(dq, stored["dq"], f"{what} dq (delta from the stored output)")
     # dQ = scale dS K grows with |K| (entries up to ~6 here, against ~1 in the
     # N(0, 1) cases), and so does its error, which the bf16 rounding of O in
     # rowsum(dO * O) dominates (present in any bf16-output implementation):

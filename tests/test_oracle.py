@@ -228,6 +228,64 @@ def test_attention_oracle_grads_match_autograd_gqa(semantics: str) -> None:
     torch.testing.assert_close(res["dv"], v.grad, rtol=1e-9, atol=1e-9)
 
 
+def _dense_attention_grads(q, k, v, doc, do):
+    """Dense-mask softmax attention with autograd (flex semantics), float64."""
+    q, k, v = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+    G = q.shape[1] // k.shape[1]
+    ke, ve = k.repeat_interleave(G, dim=1), v.repeat_interleave(G, dim=1)
+    s = (q @ ke.transpose(-1, -2)) / math.sqrt(q.shape[-1])
+    p = torch.softmax(s.masked_fill(~OA.dense_mask(doc)[:, None], -math.inf), dim=-1)
+    out = p @ ve
+    out.backward(do)
+    return out.detach(), p.detach(), ke.detach(), q.grad, k.grad, v.grad
+
+
+def test_attention_rows_oracle_matches_autograd() -> None:
+    """attention_rows (row-local out / lse / dQ) against dense autograd at chosen
+    rows, including a document's first row, a pad row and the last row."""
+    g = torch.Generator().manual_seed(6)
+    B, Hq, Hkv, S, D = 2, 4, 2, 40, 8
+    q = torch.randn(B, Hq, S, D, generator=g, dtype=torch.float64)
+    k = torch.randn(B, Hkv, S, D, generator=g, dtype=torch.float64)
+    v = torch.randn(B, Hkv, S, D, generator=g, dtype=torch.float64)
+    do = torch.randn(B, Hq, S, D, generator=g, dtype=torch.float64)
+    doc = torch.tensor([[0] * 13 + [1] * 20 + [-1] * 7, [3] * 5 + [4] * 30 + [5] * 5])
+    out, p, _, dq, _, _ = _dense_attention_grads(q, k, v, doc, do)
+    rows = [torch.tensor([0, 12, 13, 20, 35, 39]), torch.tensor([4, 5, 34, 36])]
+    res = OA.attention_rows(q, k, v, doc, do, rows)
+    lse = OA.attention(q, k, v, doc)["lse"]
+    for b in range(B):
+        torch.testing.assert_close(res["out"][b], out[b][:, rows[b]], rtol=1e-12, atol=1e-12)
+        torch.testing.assert_close(res["dq"][b], dq[b][:, rows[b]], rtol=1e-10, atol=1e-10)
+        torch.testing.assert_close(res["lse"][b], lse[b][:, rows[b]], rtol=1e-12, atol=1e-12)
+
+
+def test_attention_oracle_delta_out_closed_form() -> None:
+    """delta_out = O' shifts each row's delta by eps = rowsum(dO * (O' - O)), so
+    dS moves by -P eps: dQ by -scale * eps * (P K), dK by -scale * (P * eps)^T Q
+    (summed over the GQA group), dV not at all -- checked against dense
+    autograd plus that closed form; delta_out = O reproduces the default."""
+    g = torch.Generator().manual_seed(8)
+    B, Hq, Hkv, S, D = 1, 4, 2, 24, 8
+    q = torch.randn(B, Hq, S, D, generator=g, dtype=torch.float64)
+    k = torch.randn(B, Hkv, S, D, generator=g, dtype=torch.float64)
+    v = torch.randn(B, Hkv, S, D, generator=g, dtype=torch.float64)
+    do = torch.randn(B, Hq, S, D, generator=g, dtype=torch.float64)
+    doc = torch.tensor([[0] * 10 + [1] * 14])
+    out, p, ke, dq, dk, dv = _dense_attention_grads(q, k, v, doc, do)
+    o2 = out + 0.05 * torch.randn(out.shape, generator=g, dtype=torch.float64)
+    eps = (do * (o2 - out)).sum(-1, keepdim=True)
+    sc = 1.0 / math.sqrt(D)
+    want_dq = dq - sc * eps * (p @ ke)
+    want_dk = dk - sc * ((p * eps).transpose(-1, -2) @ q).reshape(B, Hkv, Hq // Hkv, S, D).sum(2)
+    res = OA.attention(q, k, v, doc, do, delta_out=o2)
+    torch.testing.assert_close(res["dq"], want_dq, rtol=1e-10, atol=1e-10)
+    torch.testing.assert_close(res["dk"], want_dk, rtol=1e-10, atol=1e-10)
+    torch.testing.assert_close(res["dv"], dv, rtol=1e-10, atol=1e-10)
+    same = OA.attention(q, k, v, doc, do, delta_out=out)
+    torch.testing.assert_close(same["dq"], dq, rtol=1e-10, atol=1e-10)
+
+
 def test_attention_oracle_special_cases() -> None:
     # Every token its own document: softmax over one key, out == v (GQA-mapped).
     torch.manual_seed(2)
