@@ -73,9 +73,10 @@ int pb_rmsnorm_bwd(const void *dy, int64_t dy_row_stride, const void *x,
  * as pb_rmsnorm_bwd minus `workspace`: the dW partial rows live in a static
  * per-GPU device array of PB_RMSNORM_NOALLOC_SCRATCH_BYTES (held by every GPU
  * the library runs on until the process ends).  Calls needing more
- * (pb_rmsnorm_bwd_workspace_bytes(rows, n) > the limit; any rows at
- * n <= 8192) return PB_EUNSUPPORTED.  Every call on one GPU shares the array:
- * calls that overlap on one GPU (other streams or threads) race.            */
+ * (pb_rmsnorm_bwd_workspace_bytes(rows, n) > the limit) return
+ * PB_EUNSUPPORTED; every rows count at n <= 8192 fits.  Every call on one GPU
+ * shares the array: calls that overlap on one GPU (other streams or threads)
+ * race.                                                                     */
 #define PB_RMSNORM_NOALLOC_SCRATCH_BYTES (16 * 1024 * 1024)
 int pb_rmsnorm_bwd_noalloc(const void *dy, int64_t dy_row_stride, const void *x,
                            int64_t x_row_stride, int x_dtype, const void *w,

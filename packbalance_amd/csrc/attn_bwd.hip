@@ -419,6 +419,15 @@ void attn_bwd_dkdv_pipe(BwdArgs a) {
 
   // DMA of one step: lse/delta (wave 0) and query documents (wave 1 % W)
   // first, then the Q and dO sub-tiles.
+  // One buffer resource for each of Q and dO over the rows of this
+  // workgroup's query heads (h0 .. h0 + G - 1); a step's DMA passes its byte
+  // offset as the scalar offset (the host keeps these extents below 2 GiB on
+  // this path).
+  const int h0 = hk * Gfull + g0;
+  const auto qrs = buf_rsrc(a.q.row(b, h0, 0), 0x7fffffff);
+  const auto grs = buf_rsrc(a.dout.row(b, h0, 0), 0x7fffffff);
+  const uint32_t qsh2 = (uint32_t)(a.q.sh * 2), qss2 = (uint32_t)(a.q.ss * 2);
+  const uint32_t gsh2 = (uint32_t)(a.dout.sh * 2), gss2 = (uint32_t)(a.dout.ss * 2);
   auto dma_step = [&](const DkdvStep &s, auto Rc) {
     const int64_t ro = ((int64_t)b * a.Hq + s.h) * S + s.q0;
     // lse to LDS floats [0, 32) (lanes 0-7), delta to [32, 64) (lanes 8-15):
@@ -427,10 +436,9 @@ void attn_bwd_dkdv_pipe(BwdArgs a) {
     if (wave == 0 && lane >= 8 && lane < 16) dma16(a.delta + ro, 0x7fffffff, 16 * (lane - 8), lslot(Rc));
     if (wave == (WAVES > 1 ? 1 : 0) && lane < 16)
       dma16(docb + s.q0, 0x7fffffff, 16 * lane, dslot(Rc));
-    Dma::copy_in(reinterpret_cast<const char *>(a.q.row(b, s.h, 0)), a.q.ss, qoff, s.q0, qslot(Rc),
-                 wave);
-    Dma::copy_in(reinterpret_cast<const char *>(a.dout.row(b, s.h, 0)), a.dout.ss, goff, s.q0,
-                 gslot(Rc), wave);
+    const uint32_t dh = (uint32_t)(s.h - h0), q0 = (uint32_t)s.q0;
+    Dma::copy_rs(qrs, dh * qsh2 + q0 * qss2, qoff, qslot(Rc), wave);
+    Dma::copy_rs(grs, dh * gsh2 + q0 * gss2, goff, gslot(Rc), wave);
   };
 
   // Element mask of a PARTIAL step: same document, kv <= q (q < S always).
@@ -771,18 +779,25 @@ void attn_bwd_dkdv_pairs(BwdArgs a) {
   auto step_info = [&](int t) {
     return __builtin_amdgcn_readfirstlane(steps[t < T ? t : T - 1]);
   };
+  // One buffer resource per operand over this (pack, GQA group)'s rows; a
+  // step's DMA passes its byte offset as the scalar offset (the host keeps
+  // these extents below 2 GiB on this path).
+  const auto qrs = buf_rsrc(qbase, kNoBound), grs = buf_rsrc(gbase, kNoBound);
+  const auto lrs = buf_rsrc(a.lse + rbase, kNoBound), trs = buf_rsrc(a.delta + rbase, kNoBound);
+  const auto drs = buf_rsrc(docb, kNoBound);
+  const uint32_t qsh2 = (uint32_t)(a.q.sh * 2), qss2 = (uint32_t)(a.q.ss * 2);
+  const uint32_t gsh2 = (uint32_t)(a.dout.sh * 2), gss2 = (uint32_t)(a.dout.ss * 2);
   auto dma_step = [&](int si, auto Rc) {
-    const int q0 = si & 0xfffff, g = (si >> 20) & 0xff;
-    const int64_t ro = rbase + (int64_t)g * S + q0;
-    if (wave == 0 && lane < 8) dma16(a.lse + ro, kNoBound, 16 * lane, lslot(Rc));
-    if (wave == 0 && lane >= 8 && lane < 16) dma16(a.delta + ro, kNoBound, 16 * (lane - 8), lslot(Rc));
-    if (wave == 1 && lane < 16) dma16(docb + q0, kNoBound, 16 * lane, dslot(Rc));
-    const char *qt = qbase + ((int64_t)g * a.q.sh + (int64_t)q0 * a.q.ss) * 2;
-    const char *gt = gbase + ((int64_t)g * a.dout.sh + (int64_t)q0 * a.dout.ss) * 2;
+    const uint32_t q0 = si & 0xfffff, g = (si >> 20) & 0xff;
+    const uint32_t ro = (g * (uint32_t)S + q0) * 4u;
+    if (wave == 0 && lane < 8) dma16_rs(lrs, ro, 16 * lane, lslot(Rc));
+    if (wave == 0 && lane >= 8 && lane < 16) dma16_rs(trs, ro, 16 * (lane - 8), lslot(Rc));
+    if (wave == 1 && lane < 16) dma16_rs(drs, q0 * 8u, 16 * lane, dslot(Rc));
+    const uint32_t qo = g * qsh2 + q0 * qss2, go = g * gsh2 + q0 * gss2;
 #pragma unroll
-    for (int i = 0; i < NCH; ++i) dma16(qt, kNoBound, qoff[i], qslot(Rc) + (i * 4 + wave) * 1024);
+    for (int i = 0; i < NCH; ++i) dma16_rs(qrs, qo, qoff[i], qslot(Rc) + (i * 4 + wave) * 1024);
 #pragma unroll
-    for (int i = 0; i < NCH; ++i) dma16(gt, kNoBound, goff[i], gslot(Rc) + (i * 4 + wave) * 1024);
+    for (int i = 0; i < NCH; ++i) dma16_rs(grs, go, goff[i], gslot(Rc) + (i * 4 + wave) * 1024);
   };
   const int kvmax = kt * BN + blk * 32 + 31;
   auto mask = [&](f32x16_t &sv, int si, const int64_t *qd) {
@@ -1244,6 +1259,12 @@ void attn_bwd_dq_pipe(BwdArgs a) {
   const float sl2 = a.sl2;
   const char *Kb = reinterpret_cast<const char *>(a.k.row(b, hk, 0));
   const char *Vb = reinterpret_cast<const char *>(a.v.row(b, hk, 0));
+  // One buffer resource per operand for the whole loop; a tile's DMA passes
+  // its first row's byte offset as the scalar offset (the host keeps S * row
+  // stride * 2 below 2 GiB on this path).
+  const auto krs = buf_rsrc(Kb, 0x7fffffff), vrs = buf_rsrc(Vb, 0x7fffffff);
+  const auto drs = buf_rsrc(docb, 0x7fffffff);
+  const uint32_t kss2 = (uint32_t)(a.k.ss * 2), vss2 = (uint32_t)(a.v.ss * 2);
 
   const int qi = qt * BM + wave * 32 + l32;
   const bool qvalid = qi < S;
@@ -1311,9 +1332,9 @@ void attn_bwd_dq_pipe(BwdArgs a) {
   // (The row is passed in, not computed here: calling another lambda inside
   // this generic lambda's DMA address makes clang drop the kernel's stub.)
   auto dma_sub = [&](int kv0, auto Rc) {
-    if (wave == 0 && lane < 16) dma16(docb + kv0, 0x7fffffff, 16 * lane, dslot(Rc));
-    Dma::copy_in(Kb, a.k.ss, koff, kv0, kslot(Rc), wave);
-    Dma::copy_in(Vb, a.v.ss, voff, kv0, vslot(Rc), wave);
+    if (wave == 0 && lane < 16) dma16_rs(drs, (uint32_t)kv0 * 8u, 16 * lane, dslot(Rc));
+    Dma::copy_rs(krs, (uint32_t)kv0 * kss2, koff, kslot(Rc), wave);
+    Dma::copy_rs(vrs, (uint32_t)kv0 * vss2, voff, vslot(Rc), wave);
   };
   // Element mask of a PARTIAL sub-tile: same document and kv <= q.
   // Tests and shortcuts as in attn_fwd_pipe (query rows past the sequence end
@@ -1636,7 +1657,11 @@ extern "C" int pb_attn_bwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v,
                     (reinterpret_cast<uintptr_t>(lse) & 15) == 0 &&
                     (reinterpret_cast<uintptr_t>(workspace) & 15) == 0 &&
                     32 * std::max({q->stride_s, dout->stride_s, k->stride_s, v->stride_s}) <
-                        (1LL << 30);
+                        (1LL << 30) &&
+                    s * std::max(k->stride_s, v->stride_s) * 2 < (1LL << 31) &&
+                    ((hq / hkv - 1) * std::max(q->stride_h, dout->stride_h) +
+                     s * std::max(q->stride_s, dout->stride_s)) * 2 < (1LL << 31) &&
+                    (hq / hkv) * s * 4 < (1LL << 31) && s * 8 < (1LL << 31);
   if (pipe && cfg.dq_chunk > 0) {
     a.dq_chunk = cfg.dq_chunk;
     g_q.x *= (unsigned)cfg.dq_splits;
@@ -1653,7 +1678,14 @@ extern "C" int pb_attn_bwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v,
   if (pipe) {
 #define PB_KVP(DP, W, SP) \
   hipLaunchKernelGGL((attn_bwd_dkdv_pipe<DP, W, SP>), g_kv, dim3(64 * W), 0, st, a)
-    if (cfg.pairs && (hq / hkv) * s / 32 <= kPairsMaxSteps)
+    // The paired kernel addresses one (pack, GQA group)'s Q / dO rows, and its
+    // lse / delta rows, with 32-bit byte offsets.
+    const int64_t G = hq / hkv;
+    const bool pairs_fit =
+        ((G - 1) * std::max(q->stride_h, dout->stride_h) + s * std::max(q->stride_s, dout->stride_s)) *
+                2 < (1LL << 31) &&
+        G * s * 4 < (1LL << 31);
+    if (cfg.pairs && G * s / 32 <= kPairsMaxSteps && pairs_fit)
       hipLaunchKernelGGL((attn_bwd_dkdv_pairs<128>), g_kv, dim3(256), 0, st, a);
     else if (cfg.kv_waves == 4) { if (d == 128) PB_KVP(128, 4, false); else PB_KVP(64, 4, false); }
     else if (cfg.split) {

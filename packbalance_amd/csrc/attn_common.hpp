@@ -161,6 +161,14 @@ struct TileDma {
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) dma16(tb, 0x7fffffff, off[i], dst + (i * W + wave) * 1024);
   }
+  // The same against a resource over the whole (pack, head) view: `soff` =
+  // kv0 * ss * 2 bytes (the caller keeps the view's extent below 2 GiB).
+  __device__ static __forceinline__ void copy_rs(__amdgpu_buffer_rsrc_t rs, uint32_t soff,
+                                                 const uint32_t *off, char *dst, int wave) {
+    constexpr int W = NT / 64;
+#pragma unroll
+    for (int i = 0; i < NDMA; ++i) dma16_rs(rs, soff, off[i], dst + (i * W + wave) * 1024);
+  }
 };
 
 // Exchange with lane ^ 32 without LDS (v_permlane32_swap): returns

@@ -322,6 +322,13 @@ void attn_fwd_pipe(FwdArgs a) {
   const char *Vb = reinterpret_cast<const char *>(a.v + b * a.v_sb + hk * a.v_sh);
   const int64_t *docb = a.doc + b * a.doc_sb;
   const float sl2 = a.sl2;
+  // One buffer resource per operand for the whole loop; a sub-tile's DMA
+  // passes its first row's byte offset as the scalar offset (the host keeps
+  // S * row stride * 2 below 2 GiB on this path).
+  const auto krs = buf_rsrc(Kb, (int64_t)S * a.k_ss * 2);
+  const auto vrs = buf_rsrc(Vb, (int64_t)S * a.v_ss * 2);
+  const auto drs = buf_rsrc(docb, (int64_t)S * 8);
+  const uint32_t kss2 = (uint32_t)(a.k_ss * 2), vss2 = (uint32_t)(a.v_ss * 2);
 
   uint32_t koff[NDMA], voff[NDMA];
   Dma::offsets(a.k_ss, wave, lane, koff);
@@ -529,7 +536,7 @@ void attn_fwd_pipe(FwdArgs a) {
   // kdoc of sub-tile rows kv0..kv0+31 into a ring slot: one DMA instruction
   // by 16 lanes of wave 0 (issued for every sub-tile, read for PARTIAL ones).
   auto load_kdoc = [&](int kv0, int64_t *dst) {
-    if (wave == 0 && lane < 16) dma16(docb + kv0, 0x7fffffff, 16 * lane, dst);
+    if (wave == 0 && lane < 16) dma16_rs(drs, (uint32_t)kv0 * 8u, 16 * lane, dst);
   };
 
   f32x16_t sc[NQB];
@@ -541,8 +548,8 @@ void attn_fwd_pipe(FwdArgs a) {
     auto prefetch = [&](auto Rc, int u) {
       const int e = entry(u);
       load_kdoc(row0(e, u), dslot(Rc));
-      Dma::copy_in(Kb, a.k_ss, koff, row0(e, u), kslot(Rc), wave);
-      if (decltype(Rc)::value == 0) Dma::copy_in(Vb, a.v_ss, voff, row0(e, u), vslot(Rc), wave);
+      Dma::copy_rs(krs, (uint32_t)row0(e, u) * kss2, koff, kslot(Rc), wave);
+      if (decltype(Rc)::value == 0) Dma::copy_rs(vrs, (uint32_t)row0(e, u) * vss2, voff, vslot(Rc), wave);
     };
     prefetch(I0(), 0);
     prefetch(I1(), 1);
@@ -599,8 +606,8 @@ void attn_fwd_pipe(FwdArgs a) {
       using IR1 = std::integral_constant<int, R1>;
       using IR2 = std::integral_constant<int, R2>;
       load_kdoc(row0(e3, u + 3), dslot(IR()));
-      Dma::copy_in(Kb, a.k_ss, koff, row0(e3, u + 3), kslot(IR()), wave);
-      Dma::copy_in(Vb, a.v_ss, voff, row0(e1, u + 1), vslot(IR1()), wave);
+      Dma::copy_rs(krs, (uint32_t)row0(e3, u + 3) * kss2, koff, kslot(IR()), wave);
+      Dma::copy_rs(vrs, (uint32_t)row0(e1, u + 1) * vss2, voff, vslot(IR1()), wave);
       // Fragments in the order the steps consume them: steps 0 .. kAhead-1
       // before the first MFMA, step k + kAhead during step k, so at most 12
       // LDS reads are outstanding and each MFMA waits only for its own
@@ -827,10 +834,12 @@ extern "C" int pb_attn_fwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v,
   a.part_lse = nullptr;
   dim3 grid((unsigned)(a.nqt * b * hq));
   hipStream_t st = as_stream(stream);
-  // DMA tile offsets are 32-bit: 64 rows of K / V must span < 2 GiB.
+  // DMA offsets are 32-bit: one (pack, KV head) view of K / V (S rows) and
+  // the pack's document ids must span < 2 GiB.
   const bool pipe = a.vec && (d == 64 || d == 128) && s % 64 == 0 &&
                     (reinterpret_cast<uintptr_t>(doc_ids) & 15) == 0 && doc_stride % 2 == 0 &&
-                    64 * std::max(k->stride_s, v->stride_s) < (1LL << 30);
+                    s * std::max(k->stride_s, v->stride_s) * 2 < (1LL << 31) &&
+                    s * 8 < (1LL << 31);
   if (pipe && cfg.fwd_chunk > 0) {
     PB_CHECK_ARG(workspace != nullptr, "pb_attn_fwd: workspace is required for this shape");
     a.chunk = cfg.fwd_chunk;

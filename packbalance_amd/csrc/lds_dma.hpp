@@ -57,6 +57,22 @@ __device__ __forceinline__ void dma16(const void *base, int64_t limit, uint32_t 
                                            voff, 0, 0, 0);
 }
 
+// The same DMA against a buffer resource built once (buf_rsrc) and a
+// wave-uniform byte offset `soff` (the instruction's scalar offset), so a
+// loop that walks tiles of one buffer pays one scalar add per tile instead of
+// rebuilding a 64-bit base and its resource for every instruction.  The
+// caller keeps soff + voff + 16 within the resource's `limit` bytes.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base, int64_t limit) {
+  const int lim = (int)(limit < 0x7fffffff ? limit : 0x7fffffff);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, lim, kBufWord3);
+}
+
+__device__ __forceinline__ void dma16_rs(__amdgpu_buffer_rsrc_t rs, uint32_t soff, uint32_t voff,
+                                         void *dst) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)dst, 16,
+                                           voff, soff, 0, 0);
+}
+
 // s_waitcnt vmcnt(N) with expcnt / lgkmcnt left alone: all but the N most
 // recent vector-memory operations (loads, LDS DMA) of this wave have landed.
 template <int N>

@@ -190,7 +190,7 @@ def test_multi_pack_micro_batches_match_sequential(packs_per_micro, streams, dev
     print(f"[cfg1 grouping {packs_per_micro}x{streams}] max diff {float(d.max() / gs.abs().max()):.2e}"
           f" of the largest, mean diff {float(d.mean() / gs.abs().mean()):.2e} of the mean", flush=True)
     assert d.max() <= 2e-2 * gs.abs().max()
-    assert d.mean() <= 1e-2 * gs.abs().mean()
+    assert d.mean() <= 2e-3 * gs.abs().mean()  # measured 1.1e-7 .. 1.6e-7 of the mean
     with pytest.raises(ValueError):
         TrainStep(cfg, dev, seq_len=256, store=store, packs_per_micro_batch=3)
 
