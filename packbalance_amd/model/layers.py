@@ -54,7 +54,18 @@ from packbalance_amd.model.rope import _rope
 
 WGRAD_SIDE_STREAM = True
 # The model's training forward hands its layers a WgradPlan (batched dW GEMMs).
-WGRAD_BATCHED = True
+def _wgrad_hooks_available() -> bool:
+    """The batched weight-gradient plan ends each backward pass with an autograd
+    final callback, through two private PyTorch entry points (present in the
+    torch 2.10 this build is tested with): the current graph task id and the
+    execution engine's ``queue_callback``.  Without them the layers add their
+    weight gradients one GEMM at a time."""
+    engine = getattr(torch.autograd.Variable, "_execution_engine", None)
+    return (callable(getattr(torch._C, "_current_graph_task_id", None))
+            and callable(getattr(engine, "queue_callback", None)))
+
+
+WGRAD_BATCHED = _wgrad_hooks_available()
 
 
 @contextlib.contextmanager

@@ -245,9 +245,11 @@ class LlamaForCausalLM(nn.Module):
 
     def _wgrad_plan(self, tokens: int, dt: torch.dtype, dev: torch.device):
         """The batched weight-gradient plan of one training forward (None when no
-        backward can follow, in fp32, or when ``L.WGRAD_BATCHED`` is off)."""
+        backward can follow -- grad mode off or no parameter requiring grad --,
+        in fp32, or when ``L.WGRAD_BATCHED`` is off)."""
         if (not L.WGRAD_BATCHED or dt == torch.float32 or dev.type != "cuda"
-                or not torch.is_grad_enabled() or len(self.layers) < 2):
+                or not torch.is_grad_enabled() or len(self.layers) < 2
+                or not any(p.requires_grad for p in self.parameters())):
             return None
         c = self.cfg
         nq, nkv = c.n_heads * c.head_dim, c.n_kv_heads * c.head_dim
