@@ -206,7 +206,11 @@ int pb_attn_fwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v, const pb_b
                 void *stream);
 
 /* Replaces the FlexAttention backward (dQ, dK, dV; dK/dV summed over each
- * GQA group, as enable_gqa does).  workspace: out[6] bytes of pb_attn_config.
+ * GQA group, as enable_gqa does).  workspace: out[6] bytes of pb_attn_config
+ * (at head dim 128 on large grids it also holds the bf16 dS blocks of the
+ * causal 64 x 64 tiles that dQ is formed from: B * Hkv * T * G * 8 KiB for
+ * T = (S/64)(S/64+1)/2, 17.3 GB at B 8, S 8192, Hq 32, Hkv 8; shapes past
+ * 32 GiB recompute S and dP for dQ instead).
  * kv_plan = pb_attn_plan(by_kv = 1) with the dK/dV tiles,
  * q_plan  = pb_attn_plan(by_kv = 0) with the dQ tiles of pb_attn_config.     */
 int pb_attn_bwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v, const pb_bhsd *out,

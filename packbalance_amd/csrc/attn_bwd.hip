@@ -6,7 +6,10 @@
 //   dV = P^T dO,  dP = dO V^T,  dS = P * (dP - D),
 //   dQ = scale * dS K,  dK = scale * dS^T Q.
 //
-// Two kernels, no atomics (results are run-to-run deterministic):
+// Kept dS (head dim 128 on a full grid, AttnConfig::ds): attn_bwd_delta forms
+// D, attn_bwd_dkdv_pairs<128, true> also stores its bf16 dS tiles, and
+// attn_bwd_dq_ds forms dQ = scale * dS K from them; otherwise two kernels.
+// No atomics on either path (results are run-to-run deterministic):
 //   attn_bwd_dq     one workgroup per (pack, query head, 128-row query tile),
 //                   shaped like the forward: lane <-> query row.  It first forms
 //                   D = rowsum(dO * O) from its register-resident rows (stored
@@ -61,6 +64,10 @@ struct BwdArgs {
   // partials [split][B][Hq][S][D] of query tiles with more than one chunk.
   int dq_chunk;
   float *dq_part;
+  // Kept dS blocks (AttnConfig::ds): the region of pack b, KV head hk starts
+  // at ds + (b * Hkv + hk) * ds_pair bytes.
+  char *ds;
+  int64_t ds_pair;
   int B, Hq, Hkv, S, D;
   int nqt_dq, nkt_dq, nqt_kv, nkt_kv;
   float sl2, scale;
@@ -659,7 +666,7 @@ void attn_bwd_dkdv_pipe(BwdArgs a) {
 // 2-wave kernel above.
 constexpr int kPairsMaxSteps = 1024;
 
-template <int DP>
+template <int DP, bool DS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_bwd_dkdv_pairs(BwdArgs a) {
   constexpr int NT = 256, NB = 2, BN = 32 * NB;
@@ -727,12 +734,16 @@ void attn_bwd_dkdv_pairs(BwdArgs a) {
 #pragma unroll
   for (int i = 0; i < NDB; ++i) acc[i] = zero16();
 
-  // This thread's two 16-byte chunks of a swizzled 32-row sub-tile.
+  // This thread's two 16-byte chunks of a swizzled 32-row sub-tile.  With
+  // kept dS the two P-waves issue every Q / dO chunk (four each per operand:
+  // chunk i * 128 + tid, rows 8 i + tid / 16, and the swizzle repeats every
+  // 16 rows, so chunks i and i + 2 share a lane offset): the dP-waves, whose
+  // dS stores share the in-order vmcnt, then never wait on a DMA.
   uint32_t qoff[NCH], goff[NCH];
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
     int r, c;
-    SwzTile<DP>::at(i * NT + tid, r, c);
+    SwzTile<DP>::at(DS ? i * 128 + (tid & 127) : i * NT + tid, r, c);
     qoff[i] = (uint32_t)((r * a.q.ss + c * 8) * 2);
     goff[i] = (uint32_t)((r * a.dout.ss + c * 8) * 2);
   }
@@ -794,10 +805,25 @@ void attn_bwd_dkdv_pairs(BwdArgs a) {
     if (wave == 0 && lane >= 8 && lane < 16) dma16_rs(trs, ro, 16 * (lane - 8), lslot(Rc));
     if (wave == 1 && lane < 16) dma16_rs(drs, q0 * 8u, 16 * lane, dslot(Rc));
     const uint32_t qo = g * qsh2 + q0 * qss2, go = g * gsh2 + q0 * gss2;
+    if constexpr (DS) {
+      if (pwave) {
+        // The LDS destinations are formed here, not hoisted out of the loop
+        // (eight per slot would hold 32 SGPRs).
+        int wb = wave * 1024;
+        asm volatile("" : "+s"(wb));
 #pragma unroll
-    for (int i = 0; i < NCH; ++i) dma16_rs(qrs, qo, qoff[i], qslot(Rc) + (i * 4 + wave) * 1024);
+        for (int i = 0; i < 2 * NCH; ++i)
+          dma16_rs(qrs, qo + (i >> 1) * 16 * qss2, qoff[i & 1], qslot(Rc) + i * 2048 + wb);
 #pragma unroll
-    for (int i = 0; i < NCH; ++i) dma16_rs(grs, go, goff[i], gslot(Rc) + (i * 4 + wave) * 1024);
+        for (int i = 0; i < 2 * NCH; ++i)
+          dma16_rs(grs, go + (i >> 1) * 16 * gss2, goff[i & 1], gslot(Rc) + i * 2048 + wb);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NCH; ++i) dma16_rs(qrs, qo, qoff[i], qslot(Rc) + (i * 4 + wave) * 1024);
+#pragma unroll
+      for (int i = 0; i < NCH; ++i) dma16_rs(grs, go, goff[i], gslot(Rc) + (i * 4 + wave) * 1024);
+    }
   };
   const int kvmax = kt * BN + blk * 32 + 31;
   auto mask = [&](f32x16_t &sv, int si, const int64_t *qd) {
@@ -860,7 +886,8 @@ void attn_bwd_dkdv_pairs(BwdArgs a) {
   }
   wait_vmcnt<0>();
   __syncthreads();
-  constexpr int NDMA_STEP = 2 * NCH;  // Q and dO chunks of one step (after its lse/doc DMAs)
+  // Q and dO chunks of one step per P-wave (issued after its lse/doc DMAs).
+  constexpr int NDMA_STEP = DS ? 4 * NCH : 2 * NCH;
 
   if (pwave) {
     // ---------------------------------------------------------- P-wave
@@ -919,6 +946,26 @@ void attn_bwd_dkdv_pairs(BwdArgs a) {
     // ---------------------------------------------------------- dP-wave
     f32x16_t pc = zero16();  // dP(t-1); zero before the first step
     int si2 = T > 0 ? step_info(2) : 0;
+    // Kept dS: this wave's 32 x 32 sub-block of step t-1 goes to its block
+    // (query tile, this KV tile), head g, query half; lane (KV row l32, half
+    // hh) writes its 16 query slots 16 hh .. 16 hh + 15 as two 16-byte stores.
+    char *dsreg = nullptr;
+    uint32_t dslane = 0;
+    if constexpr (DS) {
+      dsreg = a.ds + ((int64_t)b * a.Hkv + hk) * a.ds_pair;
+      dslane = (uint32_t)(blk * G * 4096 + l32 * 64 + hh * 32);
+    }
+    auto store_ds = [&](int si, const bf16x8_t (&dsf)[2]) {
+      const uint32_t q0 = si & 0xfffff, g = (si >> 20) & 0xff;
+      const uint32_t qt = q0 >> 6, qs = (q0 >> 5) & 1;
+      const uint32_t blkoff =
+          (qt * (qt + 1) / 2 + (uint32_t)kt) * (uint32_t)(G * 8192) + (g * 2 + qs) * 2048u;
+      char *p = dsreg + blkoff + dslane;
+      __builtin_nontemporal_store(*reinterpret_cast<const u32x4 *>(&dsf[0]),
+                                  reinterpret_cast<u32x4 *>(p));
+      __builtin_nontemporal_store(*reinterpret_cast<const u32x4 *>(&dsf[1]),
+                                  reinterpret_cast<u32x4 *>(p + 16));
+    };
     auto body = [&](auto Rc, int t) {
       constexpr int R = decltype(Rc)::value;
       using IR = std::integral_constant<int, R>;
@@ -946,9 +993,13 @@ void attn_bwd_dkdv_pairs(BwdArgs a) {
              bf(pp[j >> 3][(j & 7) + 1]) * (pc[j + 1] - dlt[j + 1]));
 #pragma unroll
       for (int f = 0; f < NVF; ++f) acc[f % NDB] = mfma32(dsf[f / NDB], qcol[f], acc[f % NDB]);
+      if constexpr (DS) {
+        if (t > 0) store_ds(step_info(t - 1), dsf);
+      }
       pc = pn;
       si2 = step_info(t + 3);
-      wait_vmcnt<NDMA_STEP>();
+      // With kept dS this wave issues no DMA (the P-waves wait for it).
+      if constexpr (!DS) wait_vmcnt<NDMA_STEP>();
       block_sync_nofence();
     };
     int t = 0;
@@ -978,6 +1029,9 @@ void attn_bwd_dkdv_pairs(BwdArgs a) {
            bf(pp[j >> 3][(j & 7) + 1]) * (pc[j + 1] - dlt[j + 1]));
 #pragma unroll
     for (int f = 0; f < NVF; ++f) acc[f % NDB] = mfma32(dsf[f / NDB], cfrag(qt, f), acc[f % NDB]);
+    if constexpr (DS) {
+      if (T > 0) store_ds(step_info(T - 1), dsf);
+    }
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
       const int d = 32 * db + l32;
@@ -1558,6 +1612,208 @@ __global__ __launch_bounds__(64 * WAVES) void attn_bwd_dq_wide(BwdArgs a) {
   dq_body<DP, WAVES>(a);
 }
 
+// ---------------------------------------------------------------- kept-dS dQ
+// D = rowsum(dO * O) for the kept-dS backward (there the dK/dV kernel runs
+// first and no dQ kernel forms D on the way).  DP / 8 lanes per row, eight
+// rows per lane group, all loads issued before the sums.
+template <int DP>
+__global__ __launch_bounds__(256) void attn_bwd_delta(BwdArgs a) {
+  constexpr int TPR = DP / 8, RPP = 256 / TPR, NP = 8;
+  const int64_t rows = (int64_t)a.B * a.Hq * a.S;
+  const int sub = threadIdx.x % TPR;
+  u32x4 gv[NP], ov[NP];
+  int64_t r[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    r[p] = ((int64_t)blockIdx.x * NP + p) * RPP + threadIdx.x / TPR;
+    if (r[p] < rows) {
+      const int s = (int)(r[p] % a.S);
+      const int64_t bh = r[p] / a.S;
+      const int h = (int)(bh % a.Hq), b = (int)(bh / a.Hq);
+      gv[p] = *reinterpret_cast<const u32x4 *>(a.dout.row(b, h, s) + 8 * sub);
+      ov[p] = *reinterpret_cast<const u32x4 *>(a.o.row(b, h, s) + 8 * sub);
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    float dot = 0.f;
+    if (r[p] < rows) {
+      const bf16_t *ge = reinterpret_cast<const bf16_t *>(&gv[p]);
+      const bf16_t *oe = reinterpret_cast<const bf16_t *>(&ov[p]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) dot += (float)ge[i] * (float)oe[i];
+    }
+#pragma unroll
+    for (int m = TPR / 2; m >= 1; m >>= 1) dot += __shfl_xor(dot, m, TPR);
+    if (r[p] < rows && sub == 0) a.delta[r[p]] = dot;
+  }
+}
+
+// dQ = scale * dS K over the kept dS blocks (AttnConfig::ds, head dim 128).
+// One workgroup per (pack, four query heads of one GQA group, 64-row query
+// tile): wave w owns head 4 quad + w / 2 and query half w % 2, accumulating
+// dQ^T = K^T dS^T (lane <-> query slot, 4 x 16 registers <-> head dim) over
+// the tile's plan list, one 32-row KV half per step.  Per step the K half
+// (8 KiB, swizzled) and the eight dS sub-blocks of the quad at that KV half
+// (16 KiB, contiguous in HBM) arrive by LDS DMA through a 3-slot ring; both
+// operands are read with ds_read_b64_tr_b16 (K^T columns as in the dQ
+// kernel, dS^T columns from the 32 x 32 sub-blocks at a 64-byte pitch), so
+// the k slots of both follow pi.  No recomputation: one MFMA product per
+// pair where the dQ kernel runs three, and the kernel streams the dS blocks
+// (2 bytes per pair and head) from HBM.
+constexpr int kDsMaxTiles = kPairsMaxSteps / 8;  // 64-row KV tiles per list (G >= 4)
+
+template <int DP>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4)))
+void attn_bwd_dq_ds(BwdArgs a) {
+  static_assert(DP == 128, "head dim 128");
+  constexpr int NT = 512, NDB = DP / 32;
+  constexpr int KB = 32 * DP * 2;  // one 32-row K half
+  constexpr int SB = 8 * 2048;     // 4 heads x 2 query halves of 32 x 32 bf16
+  constexpr int64_t kNoBound = 0x7fffffff;
+  using Dma = TileDma<DP, 32, NT>;
+  static_assert(Dma::NDMA == 1, "one K chunk per thread");
+  __shared__ __align__(16) char ks0[KB], ks1[KB], ks2[KB];
+  __shared__ __align__(16) char ss0[SB], ss1[SB], ss2[SB];
+  __shared__ int32_t ents[kDsMaxTiles];
+  auto kslot = [&](auto Rc) -> char * {
+    constexpr int R = decltype(Rc)::value;
+    if constexpr (R == 0) return ks0; else if constexpr (R == 1) return ks1; else return ks2;
+  };
+  auto sslot = [&](auto Rc) -> char * {
+    constexpr int R = decltype(Rc)::value;
+    if constexpr (R == 0) return ss0; else if constexpr (R == 1) return ss1; else return ss2;
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int gg = wave >> 1, qs = wave & 1;
+  const int hh = lane >> 5;
+  const int G = a.Hq / a.Hkv, nquad = a.Hq / 4, nqt = a.nqt_dq;
+  // Grid: (pack, quad) pairs spread over the 8 XCDs (workgroup i runs on XCD
+  // i % 8), each XCD walking its pairs' query tiles late first, so the
+  // workgroups resident on one XCD read the same KV head's K halves from its L2.
+  int qt, pr;
+  {
+    const int bid = (int)blockIdx.x, npairs = a.B * nquad;
+    if (npairs % 8 == 0) {
+      const int x = bid & 7, j = bid >> 3;
+      pr = (j / nqt) * 8 + x;
+      qt = nqt - 1 - (j - (j / nqt) * nqt);
+    } else {
+      pr = bid / nqt;
+      qt = nqt - 1 - (bid - pr * nqt);
+    }
+  }
+  const int b = pr / nquad, quad = pr - (pr / nquad) * nquad;
+  const int h0 = 4 * quad, hk = h0 / G, g0 = h0 - hk * G;
+  const int h = h0 + gg;
+  const int cnt = a.qcnt[b * nqt + qt];
+  const int U = 2 * cnt;  // 32-row KV halves
+  {
+    const int32_t *lst = a.qlist + ((int64_t)b * nqt + qt) * a.nkt_dq;
+    for (int i = tid; i < cnt; i += NT) ents[i] = lst[i];
+  }
+  const char *Kb = reinterpret_cast<const char *>(a.k.row(b, hk, 0));
+  const auto krs = buf_rsrc(Kb, kNoBound);
+  const auto drs = buf_rsrc(a.ds + ((int64_t)b * a.Hkv + hk) * a.ds_pair, kNoBound);
+  const uint32_t kss2 = (uint32_t)(a.k.ss * 2);
+  const uint32_t tri = (uint32_t)(qt * (qt + 1) / 2);
+  const uint32_t blkb = (uint32_t)(G * 8192), halfb = (uint32_t)(G * 4096), quadb = (uint32_t)(g0 * 4096);
+  uint32_t koff[1];
+  Dma::offsets(a.k.ss, wave, lane, koff);
+  const uint32_t soff0 = (uint32_t)((wave * 64 + lane) * 16), soff1 = soff0 + 8 * 1024;
+  // ds_read_b64_tr_b16 addresses (see lds_col_frag): K^T of head-dim block
+  // db (swizzled K half), dS^T of this wave's sub-block (64-byte pitch).
+  int coffs[NDB][2], soffs[2];
+  {
+    const int j = lane & 15, g = lane >> 4;
+    const int row = 4 * hh + (j >> 2);
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const int col = 32 * db + 16 * (g & 1) + 4 * (j & 3);
+      coffs[db][0] = SwzTile<DP>::off(row, col);
+      coffs[db][1] = SwzTile<DP>::off(row + 8, col);
+      asm volatile("" : "+v"(coffs[db][0]), "+v"(coffs[db][1]));
+    }
+    const int col = 16 * (g & 1) + 4 * (j & 3);
+    soffs[0] = (gg * 2 + qs) * 2048 + (row * 32 + col) * 2;
+    soffs[1] = soffs[0] + 8 * 64;
+    asm volatile("" : "+v"(soffs[0]), "+v"(soffs[1]));
+  }
+  auto trd = [](const char *p0, const char *p1) {
+    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)p0);
+    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)p1);
+    typedef short i16x8_t __attribute__((ext_vector_type(8)));
+    i16x8_t r = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return *reinterpret_cast<bf16x8_t *>(&r);
+  };
+  auto dma_sub = [&](int u, auto Rc) {
+    const int uu = u < U ? u : U - 1;
+    const int e = __builtin_amdgcn_readfirstlane(ents[uu >> 1]);
+    const uint32_t kt = (uint32_t)plan_tile(e), half = (uint32_t)(uu & 1);
+    Dma::copy_rs(krs, (kt * 64 + half * 32) * kss2, koff, kslot(Rc), wave);
+    const uint32_t so = (tri + kt) * blkb + half * halfb + quadb;
+    dma16_rs_nt(drs, so, soff0, sslot(Rc) + wave * 1024);
+    dma16_rs_nt(drs, so, soff1, sslot(Rc) + (8 + wave) * 1024);
+  };
+  f32x16_t acc[NDB];
+#pragma unroll
+  for (int i = 0; i < NDB; ++i) acc[i] = zero16();
+  __syncthreads();  // the list
+  if (U > 0) {
+    dma_sub(0, I0());
+    dma_sub(1, I1());
+    wait_vmcnt<3>();
+    __syncthreads();
+    auto body = [&](auto Rc, int u) {
+      constexpr int R = decltype(Rc)::value;
+      using IR2 = std::integral_constant<int, (R + 2) % 3>;
+      __builtin_amdgcn_sched_barrier(0);
+      dma_sub(u + 2, IR2());
+      const char *kt = kslot(Rc), *st = sslot(Rc);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const bf16x8_t bfr = trd(st + soffs[0] + ks * 16 * 64, st + soffs[1] + ks * 16 * 64);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          const char *kb = kt + ks * 16 * DP * 2;
+          acc[db] = mfma32(trd(kb + coffs[db][0], kb + coffs[db][1]), bfr, acc[db]);
+        }
+      }
+      wait_vmcnt<3>();
+      block_sync_nofence();
+    };
+    int u = 0;
+    for (; u + 3 <= U; u += 3) {
+      body(I0(), u);
+      body(I1(), u + 1);
+      body(I2(), u + 2);
+    }
+    if (u < U) { body(I0(), u); ++u; }
+    if (u < U) { body(I1(), u); ++u; }
+    wait_vmcnt<0>();
+  }
+  // Lane <-> query slot sl (row 8 (sl % 16 / 4) + 4 (sl / 16) + sl % 4 of the
+  // query half), register j <-> head-dim row 8 (j / 4) + 4 hh + j % 4.
+  const int sl = lane & 31;
+  const int q = qt * 64 + qs * 32 + 8 * ((sl & 15) >> 2) + 4 * (sl >> 4) + (sl & 3);
+  bf16_t *qrow = a.dq.row(b, h, q);
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int jq = 0; jq < 4; ++jq) {
+      typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+      bf16x4_t o4;
+#pragma unroll
+      for (int x = 0; x < 4; ++x) o4[x] = (bf16_t)(acc[db][4 * jq + x] * a.scale);
+      *reinterpret_cast<bf16x4_t *>(qrow + 32 * db + 8 * jq + 4 * hh) = o4;
+    }
+}
+
 View view_of(const pb_bhsd *t) {
   View v;
   v.p = static_cast<bf16_t *>(t->data);
@@ -1625,6 +1881,8 @@ extern "C" int pb_attn_bwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v,
   a.kv_tile = (int)cfg.kv_tile();
   a.dq_chunk = 0;
   a.dq_part = reinterpret_cast<float *>(ws + attn_bwd_dq_part_offset(b, hq, s, d, cfg.split != 0));
+  a.ds = nullptr;
+  a.ds_pair = 0;
   a.doc = doc_ids;
   a.doc_sb = doc_stride;
   a.qcnt = q_plan_counts; a.qlist = q_plan_lists;
@@ -1662,6 +1920,29 @@ extern "C" int pb_attn_bwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v,
                     ((hq / hkv - 1) * std::max(q->stride_h, dout->stride_h) +
                      s * std::max(q->stride_s, dout->stride_s)) * 2 < (1LL << 31) &&
                     (hq / hkv) * s * 4 < (1LL << 31) && s * 8 < (1LL << 31);
+  // The paired kernel addresses one (pack, GQA group)'s Q / dO rows, and its
+  // lse / delta rows, with 32-bit byte offsets.
+  const int64_t G = hq / hkv;
+  const bool pairs_fit =
+      ((G - 1) * std::max(q->stride_h, dout->stride_h) + s * std::max(q->stride_s, dout->stride_s)) *
+              2 < (1LL << 31) &&
+      G * s * 4 < (1LL << 31);
+  const bool pairs = pipe && cfg.pairs && G * s / 32 <= kPairsMaxSteps && pairs_fit;
+  if (pairs && cfg.ds) {
+    // Kept dS: D, then dK/dV storing dS, then dQ = scale * dS K.
+    a.ds = ws + delta_bytes;
+    a.ds_pair = ds_pair_bytes(G, s);
+    const int64_t rows = b * hq * s;
+    hipLaunchKernelGGL(attn_bwd_delta<128>, dim3((unsigned)((rows + 127) / 128)), dim3(256), 0, st, a);
+    rc = launch_status("pb_attn_bwd(delta)");
+    if (rc) return rc;
+    hipLaunchKernelGGL((attn_bwd_dkdv_pairs<128, true>), g_kv, dim3(256), 0, st, a);
+    rc = launch_status("pb_attn_bwd(dkdv)");
+    if (rc) return rc;
+    hipLaunchKernelGGL(attn_bwd_dq_ds<128>, dim3((unsigned)(b * (hq / 4) * a.nqt_dq)), dim3(512), 0,
+                       st, a);
+    return launch_status("pb_attn_bwd(dq)");
+  }
   if (pipe && cfg.dq_chunk > 0) {
     a.dq_chunk = cfg.dq_chunk;
     g_q.x *= (unsigned)cfg.dq_splits;
@@ -1678,15 +1959,8 @@ extern "C" int pb_attn_bwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v,
   if (pipe) {
 #define PB_KVP(DP, W, SP) \
   hipLaunchKernelGGL((attn_bwd_dkdv_pipe<DP, W, SP>), g_kv, dim3(64 * W), 0, st, a)
-    // The paired kernel addresses one (pack, GQA group)'s Q / dO rows, and its
-    // lse / delta rows, with 32-bit byte offsets.
-    const int64_t G = hq / hkv;
-    const bool pairs_fit =
-        ((G - 1) * std::max(q->stride_h, dout->stride_h) + s * std::max(q->stride_s, dout->stride_s)) *
-                2 < (1LL << 31) &&
-        G * s * 4 < (1LL << 31);
-    if (cfg.pairs && G * s / 32 <= kPairsMaxSteps && pairs_fit)
-      hipLaunchKernelGGL((attn_bwd_dkdv_pairs<128>), g_kv, dim3(256), 0, st, a);
+    if (pairs)
+      hipLaunchKernelGGL((attn_bwd_dkdv_pairs<128, false>), g_kv, dim3(256), 0, st, a);
     else if (cfg.kv_waves == 4) { if (d == 128) PB_KVP(128, 4, false); else PB_KVP(64, 4, false); }
     else if (cfg.split) {
       // Lists of >= kKvChunkSteps steps are walked as two halves by two workgroups.

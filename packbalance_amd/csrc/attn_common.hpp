@@ -261,9 +261,28 @@ inline bool views_vectorizable(int64_t d, std::initializer_list<const pb_bhsd *>
 // tiles, one workgroup per chunk (fwd_splits = most chunks any list can
 // need); a tile with more than one chunk leaves normalised fp32 partial
 // outputs and their log-sum-exps, merged by a combine kernel.
+// Kept dS (head dim 128): one block of bf16 dS per (pack, KV head, 64-row
+// query tile, 64-row KV tile) at or below the diagonal, laid out
+// [KV half][head of the GQA group][query half][32 KV rows][32 query slots]
+// (2 KiB per 32 x 32 sub-block, G * 8 KiB per block), blocks addressed
+// densely over the causal triangle: block (qt, kt) at qt (qt + 1) / 2 + kt.
+// Only the plan's non-empty blocks are written and read.  Query slot s of a
+// sub-block holds query row 8 ((s % 16) / 4) + 4 (s / 16) + s % 4 (the row
+// order of the dK/dV kernel's dS accumulators).
+constexpr int64_t kDsMaxBytes = 32LL << 30;
+inline int64_t ds_tri(int64_t s) { return (s / 64) * (s / 64 + 1) / 2; }
+inline int64_t ds_pair_bytes(int64_t g, int64_t s) { return ds_tri(s) * g * 8192; }
+inline int64_t ds_bytes(int64_t b, int64_t hq, int64_t hkv, int64_t s) {
+  return b * hkv * ds_pair_bytes(hq / hkv, s);
+}
+
 struct AttnConfig {
   int fwd_waves, dq_waves, kv_waves, split;
   int pairs;  // head dim 128 on a full grid: dK/dV by attn_bwd_dkdv_pairs on 64-row KV tiles
+  // dS kept: the paired dK/dV kernel stores its bf16 dS tiles and dQ = scale * dS K
+  // is a streaming pass over them (attn_bwd_dq_ds) instead of a kernel that
+  // recomputes S and dP; D = rowsum(dO * O) then comes from attn_bwd_delta.
+  int ds;
   int fwd_chunk, fwd_splits;  // 0 / 1: no forward KV split
   int dq_chunk, dq_splits;    // the same for the (q-major) dQ kernel
   int fwd_q_tile() const { return 32 * fwd_waves; }
@@ -284,6 +303,9 @@ inline AttnConfig attn_config(int64_t b, int64_t hq, int64_t hkv, int64_t s, int
   // two workgroups per CU (the KV tile of the 2-wave kernels).
   c.pairs = (d == 128 && c.kv_waves == 4) ? 1 : 0;
   if (c.pairs) c.kv_waves = 2;
+  c.ds = (c.pairs && (hq / hkv) % 4 == 0 && ds_pair_bytes(hq / hkv, s) < (1LL << 31) &&
+          ds_bytes(b, hq, hkv, s) <= kDsMaxBytes) ? 1 : 0;
+  if (c.ds) c.dq_waves = 2;  // dQ on the 64-row query tiles of the dS blocks
   // Aim for ~2048 chunk workgroups over all lists, but at least 4 KV tiles
   // each (a chunk also pays the prologue and the merge).  Measured on the
   // cfg2 step (two [2, 2048] micro-batches on two streams; attention kernel
@@ -317,7 +339,8 @@ inline int64_t attn_fwd_workspace(int64_t b, int64_t hq, int64_t hkv, int64_t s,
 // Workspace of pb_attn_bwd: delta [b, hq, s] fp32, then (split) dK and dV
 // partials [b, hq, s, d] fp32 each and a second such pair (the second halves
 // of long KV lists), then (dQ KV split) dQ partials [dq_splits, b, hq, s, d]
-// fp32.
+// fp32; with kept dS (AttnConfig::ds, which excludes both splits) the dS
+// blocks follow delta.
 inline int64_t attn_bwd_dq_part_offset(int64_t b, int64_t hq, int64_t s, int64_t d, bool split) {
   int64_t bytes = (b * hq * s * 4 + 255) / 256 * 256;
   // split: dK and dV partials, and a second pair for lists walked in two halves
@@ -328,6 +351,7 @@ inline int64_t attn_bwd_dq_part_offset(int64_t b, int64_t hq, int64_t s, int64_t
 inline int64_t attn_bwd_workspace(int64_t b, int64_t hq, int64_t hkv, int64_t s, int64_t d) {
   const AttnConfig c = attn_config(b, hq, hkv, s, d);
   int64_t bytes = attn_bwd_dq_part_offset(b, hq, s, d, c.split != 0);
+  if (c.ds) bytes += ds_bytes(b, hq, hkv, s);  // the kept dS blocks after delta
   if (c.dq_chunk) bytes += (int64_t)c.dq_splits * b * hq * s * d * 4;
   return bytes;
 }

@@ -73,6 +73,15 @@ __device__ __forceinline__ void dma16_rs(__amdgpu_buffer_rsrc_t rs, uint32_t sof
                                            voff, soff, 0, 0);
 }
 
+// dma16_rs for data read exactly once: the non-temporal cache policy (nt)
+// marks the lines for early eviction, so a stream does not push re-used
+// tiles out of L2.
+__device__ __forceinline__ void dma16_rs_nt(__amdgpu_buffer_rsrc_t rs, uint32_t soff,
+                                            uint32_t voff, void *dst) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)dst, 16,
+                                           voff, soff, 0, 2);
+}
+
 // s_waitcnt vmcnt(N) with expcnt / lgkmcnt left alone: all but the N most
 // recent vector-memory operations (loads, LDS DMA) of this wave have landed.
 template <int N>

@@ -12,6 +12,7 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
 import pytest
 import torch
 
@@ -251,6 +252,28 @@ def test_attention_large_grid_layouts(layout, dev) -> None:
     _close(dk[:, g : g + 1], ref["dk"], "dk")
     _close(dv[:, g : g + 1], ref["dv"], "dv")
     assert torch.isfinite(out.float()).all()
+
+
+def test_attention_kept_ds_two_quads_per_kv_head(dev) -> None:
+    """Kept-dS backward with G = 8 (each KV head's dS blocks hold two quads of
+    query heads, and two dQ workgroups read them), lognormal packs and a
+    padded tail: every query head of KV head 1, pack 2, against the oracle."""
+    B, Hq, Hkv, S, D = 8, 16, 2, 4096, 128
+    rng = np.random.default_rng(5)
+    lens = [W.fill_sequential(rng, S, np.log(512), 1.0, 16, S) for _ in range(B)]
+    lens[2] = lens[2][:-1]  # padded tail
+    doc = W.doc_ids_from_lengths(lens, S).to(dev)
+    q, k, v, do = _inputs(B, Hq, Hkv, S, D, dev, seed=8)
+    out, dq, dk, dv = _run(q, k, v, do, doc)
+    sl, g = slice(2, 3), 1
+    hs = slice(8 * g, 8 * g + 8)
+    ref = OA.attention(q[sl, hs], k[sl, g : g + 1], v[sl, g : g + 1], doc[sl].cpu(), do[sl, hs],
+                       dtype=torch.float32)
+    _close(out[sl, hs], ref["out"], "out")
+    _close(dq[sl, hs], ref["dq"], "dq")
+    _close(dk[sl, g : g + 1], ref["dk"], "dk")
+    _close(dv[sl, g : g + 1], ref["dv"], "dv")
+    assert torch.isfinite(dq.float()).all()
 
 
 @pytest.mark.parametrize("D", [64, 128])

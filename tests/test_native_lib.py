@@ -91,3 +91,27 @@ def test_ce_backward_split_k_choice_on_host() -> None:
     assert splits(4096, 32000, 768, 32000) == 8
     assert splits(16384, 128256, 4096, 8192) == 1
     assert splits(512, 512, 128, 512) == 1  # a 512-column chunk cannot be split
+
+
+def test_attention_kept_ds_config_on_host() -> None:
+    """pb_attn_config: head dim 128 on a full grid with G % 4 == 0 keeps dS (64-row
+    dQ tiles; workspace = delta + one G * 8 KiB block per causal 64 x 64 tile and
+    (pack, KV head)); other shapes keep the recompute backward."""
+    from packbalance_amd.model.attention import attn_config
+
+    def ws_ds(b, hq, hkv, s):
+        tri = (s // 64) * (s // 64 + 1) // 2
+        return (b * hq * s * 4 + 255) // 256 * 256 + b * hkv * tri * (hq // hkv) * 8192
+
+    c = attn_config(8, 32, 8, 8192, 128)  # cfg3
+    assert c["tiles"][2] == (64, 64) and c["workspace"] == ws_ds(8, 32, 8, 8192)
+    c = attn_config(8, 16, 2, 4096, 128)  # G = 8: two quads per KV head
+    assert c["tiles"][2] == (64, 64) and c["workspace"] == ws_ds(8, 16, 2, 4096)
+    for shape in [(2, 12, 4, 2048, 64),      # cfg2 micro-batch: D 64, G 3
+                  (1, 8, 2, 1024, 128)]:     # small grid (split dK/dV partials)
+        assert attn_config(*shape)["workspace"] != ws_ds(*shape[:4]), shape
+    for shape in [(8, 24, 8, 8192, 128),     # G = 3
+                  (8, 32, 8, 16384, 128)]:   # dS blocks beyond the 32 GiB cap
+        c = attn_config(*shape)
+        assert c["tiles"][2] == (128, 64) and c["workspace"] == (8 * shape[1] * shape[3] * 4), shape
+
