@@ -21,7 +21,8 @@ runs on):
 The ``roofline`` object is document-masked attention fwd+bwd at cfg3 (MFMA-bound),
 the headline "masked-attn TFLOP/s": ``achieved`` = 12*D*Hq*P FLOPs per
 forward+backward / the summed HIP-event durations of the two entry points
-(pb_attn_fwd: the forward kernel; pb_attn_bwd: the dQ and dK/dV kernels);
+(pb_attn_fwd: the forward kernel; pb_attn_bwd: at cfg3 the delta, dK/dV
+(storing dS) and dQ-from-dS kernels);
 ``traffic`` = HBM-side bytes of the same kernels per fwd+bwd from the committed
 rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/attention_cfg3_hbm_counters.txt).
 
@@ -629,7 +630,8 @@ def main() -> int:
         a = kernels["attention"]
         roofline = {"bound": "mfma",
                     "kernel": "document-masked attention fwd+bwd at cfg3: pb_attn_fwd + pb_attn_bwd "
-                              "(attn_fwd_pipe, attn_bwd_dq_pipe, attn_bwd_dkdv_pairs)",
+                              "(attn_fwd_pipe; attn_bwd_delta, attn_bwd_dkdv_pairs<128, true>, "
+                              "attn_bwd_dq_ds)",
                     "achieved": a["fwd_bwd_tflops"], "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                     "frac": a["fwd_bwd_tflops"] / PEAK_BF16_TFLOPS,
                     "traffic": counter_traffic(ATTN_KERNELS),
