@@ -329,6 +329,26 @@ int pb_add_rmsnorm_bwd(const void *dy, int64_t dy_row_stride, int dy_dtype, cons
                        int ddelta_dtype, void *dw, int dw_accumulate, void *workspace,
                        int64_t rows, int64_t n, void *stream);
 
+/* The same backward with the dw reduction left to the caller (no reference
+ * counterpart: the reference's rmsnorm backward sums dw in a second PyTorch
+ * pass, packbalance/kernels/rmsnorm.py:106-118, once per norm).  dx and
+ * ddelta as pb_add_rmsnorm_bwd; `partials` (pb_add_rmsnorm_bwd_workspace_bytes
+ * bytes) receives the fp32 per-workgroup partial rows of dw.
+ * pb_rmsnorm_dw_reduce_batched then adds, for i < count, the column sums of
+ * the table at partials + i * problem_stride (floats) to the fp32 dw[i]
+ * (a host array of count device pointers), each problem's table written by
+ * pb_add_rmsnorm_bwd_partials with the same rows and n -- one launch per 32
+ * problems instead of one per norm, with the same bits as dw_accumulate.   */
+int pb_add_rmsnorm_bwd_partials(const void *dy, int64_t dy_row_stride, int dy_dtype,
+                                const void *h, int64_t h_row_stride, int h_dtype, const void *w,
+                                int w_dtype, const float *rstd, const void *dres,
+                                int64_t dres_row_stride, void *dx, int64_t dx_row_stride,
+                                void *ddelta, int64_t ddelta_row_stride, int ddelta_dtype,
+                                float *partials, int64_t rows, int64_t n, void *stream);
+int pb_rmsnorm_dw_reduce_batched(const float *partials, int64_t problem_stride,
+                                 float *const *dw, int64_t count, int64_t rows, int64_t n,
+                                 void *stream);
+
 /* ---- Model inputs of packs, built on the device --------------------------
  * Replaces packbalance/data/dataset.py:33-76 (PackedDataset.__getitem__) for
  * a batch of packs, reading a token store resident in device memory (the

@@ -128,6 +128,12 @@ SIGNATURES: dict[str, tuple] = {
         [_p, _i64, _i32, _p, _i64, _i32, _p, _i32, _p, _p, _i64, _p, _i64, _p, _i64, _i32, _p, _i32,
          _p, _i64, _i64, _p],
     ),
+    "pb_add_rmsnorm_bwd_partials": (
+        _i32,
+        [_p, _i64, _i32, _p, _i64, _i32, _p, _i32, _p, _p, _i64, _p, _i64, _p, _i64, _i32, _p,
+         _i64, _i64, _p],
+    ),
+    "pb_rmsnorm_dw_reduce_batched": (_i32, [_p, _i64, _p, _i64, _i64, _i64, _p]),
     "pb_pack_tensors": (
         _i32,
         [_p, _i32, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p],

@@ -20,6 +20,7 @@
 // forward streams with non-temporal loads and stores, the backward with
 // cached ones (at [4096, 768] rows of the model: backward 15.7 -> 14.9 us
 // cached, forward 10.5 -> 10.9 us, so each keeps its faster form).
+#include <algorithm>
 #include <initializer_list>
 #include <utility>
 
@@ -321,11 +322,12 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_bwd_loop(AddNormBwd a) {
 // is bound by load latency, not bandwidth), then the 16 wave sums are
 // folded in LDS in a fixed order, so the result is deterministic.
 constexpr int kRedWaves = 16;
-__global__ __launch_bounds__(64 * kRedWaves) void add_rmsnorm_dw_reduce(
-    const float *__restrict__ partial, char *dw, int wdt, int nparts, int n, int accumulate) {
-  __shared__ float red[kRedWaves][64];
+// The column sum of workgroup column block `blk`; valid in wave 0 (returns
+// false for the other waves and for columns past n).
+__device__ __forceinline__ bool dw_column_sum(const float *__restrict__ partial, int nparts, int n,
+                                              int blk, float (&red)[kRedWaves][64], float &t) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int col = blockIdx.x * 64 + lane;
+  const int col = blk * 64 + lane;
   float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (col < n) {
     int p = w;
@@ -337,15 +339,39 @@ __global__ __launch_bounds__(64 * kRedWaves) void add_rmsnorm_dw_reduce(
   }
   red[w][lane] = ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
   __syncthreads();
-  if (w == 0 && col < n) {
-    float t = 0.f;
+  if (w != 0 || col >= n) return false;
+  t = 0.f;
 #pragma unroll
-    for (int g = 0; g < kRedWaves; ++g) t += red[g][lane];
-    if (accumulate)
-      reinterpret_cast<float *>(dw)[col] += t;
-    else
-      st1(dw + (int64_t)col * esize(wdt), wdt, t);
-  }
+  for (int g = 0; g < kRedWaves; ++g) t += red[g][lane];
+  return true;
+}
+
+__global__ __launch_bounds__(64 * kRedWaves) void add_rmsnorm_dw_reduce(
+    const float *__restrict__ partial, char *dw, int wdt, int nparts, int n, int accumulate) {
+  __shared__ float red[kRedWaves][64];
+  float t;
+  if (!dw_column_sum(partial, nparts, n, blockIdx.x, red, t)) return;
+  const int col = blockIdx.x * 64 + (threadIdx.x & 63);
+  if (accumulate)
+    reinterpret_cast<float *>(dw)[col] += t;
+  else
+    st1(dw + (int64_t)col * esize(wdt), wdt, t);
+}
+
+// The same reduction for up to kDwBatch problems in one launch (grid.y =
+// problem): dw_i[c] += sum_p partial_i[p, c], partial_i = partials + i *
+// stride, fp32 dw.  The per-column arithmetic is the kernel's above, so a
+// deferred reduction gives the same bits as the immediate one.
+constexpr int kDwBatch = 32;
+struct DwBatch {
+  float *dw[kDwBatch];
+};
+__global__ __launch_bounds__(64 * kRedWaves) void rmsnorm_dw_reduce_batched(
+    const float *__restrict__ partials, int64_t stride, DwBatch dws, int nparts, int n) {
+  __shared__ float red[kRedWaves][64];
+  float t;
+  if (!dw_column_sum(partials + blockIdx.y * stride, nparts, n, blockIdx.x, red, t)) return;
+  dws.dw[blockIdx.y][blockIdx.x * 64 + (threadIdx.x & 63)] += t;
 }
 
 // dw = 0 (or unchanged when accumulating) for an empty batch.
@@ -428,35 +454,17 @@ extern "C" int64_t pb_add_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t n) {
   return (int64_t)pb::bwd_nwg(rows, rpw) * n * (int64_t)sizeof(float);
 }
 
-extern "C" int pb_add_rmsnorm_bwd(const void *dy, int64_t dy_row_stride, int dy_dtype,
-                                  const void *h, int64_t h_row_stride, int h_dtype, const void *w,
-                                  int w_dtype, const float *rstd, const void *dres,
-                                  int64_t dres_row_stride, void *dx, int64_t dx_row_stride,
-                                  void *ddelta, int64_t ddelta_row_stride, int ddelta_dtype,
-                                  void *dw, int dw_accumulate, void *workspace, int64_t rows,
-                                  int64_t n, void *stream) {
-  using namespace pb;
-  clear_error();
-  PB_CHECK_ARG(valid_dtype(dy_dtype) && valid_dtype(h_dtype) && valid_dtype(w_dtype) &&
-                   (!ddelta || valid_dtype(ddelta_dtype)),
-               "pb_add_rmsnorm_bwd: bad dtype");
-  PB_CHECK_ARG(rows >= 0 && n > 0, "pb_add_rmsnorm_bwd: bad shape");
-  PB_CHECK_SUPPORTED(n <= 65536, "RMSNorm feature dimension is too large for this kernel");
-  PB_CHECK_ARG(w && dw, "pb_add_rmsnorm_bwd: null weight or dw");
-  PB_CHECK_ARG(!dw_accumulate || w_dtype == PB_F32,
-               "pb_add_rmsnorm_bwd: dw_accumulate needs an fp32 weight (and dw)");
-  PB_CHECK_ARG(dy_row_stride >= n && h_row_stride >= n && dx_row_stride >= n &&
-                   (!dres || dres_row_stride >= n) && (!ddelta || ddelta_row_stride >= n),
-               "pb_add_rmsnorm_bwd: row stride < n");
-  hipStream_t st = as_stream(stream);
-  if (rows == 0) {
-    if (!dw_accumulate)
-      hipLaunchKernelGGL(add_rmsnorm_dw_zero, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                         static_cast<char *>(dw), w_dtype, (int)n);
-    return launch_status("pb_add_rmsnorm_bwd(empty)");
-  }
-  PB_CHECK_ARG(dy && h && rstd && dx, "pb_add_rmsnorm_bwd: null argument");
-  PB_CHECK_ARG(workspace != nullptr, "pb_add_rmsnorm_bwd: workspace is required");
+namespace pb {
+namespace {
+// The backward kernel alone: dx, ddelta and the dw partials [nwg, n] in
+// `workspace` (arguments checked by the caller, rows > 0).  Returns nwg or
+// a negative status.
+int add_rmsnorm_bwd_rows(const void *dy, int64_t dy_row_stride, int dy_dtype, const void *h,
+                         int64_t h_row_stride, int h_dtype, const void *w, int w_dtype,
+                         const float *rstd, const void *dres, int64_t dres_row_stride, void *dx,
+                         int64_t dx_row_stride, void *ddelta, int64_t ddelta_row_stride,
+                         int ddelta_dtype, void *workspace, int64_t rows, int64_t n,
+                         hipStream_t st, const char *what) {
   AddNormBwd a;
   a.dy = static_cast<const char *>(dy);
   a.h = static_cast<const char *>(h);
@@ -486,10 +494,113 @@ extern "C" int pb_add_rmsnorm_bwd(const void *dy, int64_t dy_row_stride, int dy_
     case 4: hipLaunchKernelGGL((add_rmsnorm_bwd_reg<4>), grid, dim3(kThreads), 0, st, a); break;
     default: hipLaunchKernelGGL(add_rmsnorm_bwd_loop, grid, dim3(kThreads), 0, st, a);
   }
-  int s = launch_status("pb_add_rmsnorm_bwd");
-  if (s) return s;
+  const int s = launch_status(what);
+  return s ? -s : nwg;
+}
+
+int check_bwd_args(const char *what, int dy_dtype, int h_dtype, int w_dtype, const void *ddelta,
+                   int ddelta_dtype, int64_t rows, int64_t n, int64_t dy_row_stride,
+                   int64_t h_row_stride, int64_t dx_row_stride, const void *dres,
+                   int64_t dres_row_stride, int64_t ddelta_row_stride) {
+  PB_CHECK_ARG(valid_dtype(dy_dtype) && valid_dtype(h_dtype) && valid_dtype(w_dtype) &&
+                   (!ddelta || valid_dtype(ddelta_dtype)),
+               "%s: bad dtype", what);
+  PB_CHECK_ARG(rows >= 0 && n > 0, "%s: bad shape", what);
+  PB_CHECK_SUPPORTED(n <= 65536, "RMSNorm feature dimension is too large for this kernel");
+  PB_CHECK_ARG(dy_row_stride >= n && h_row_stride >= n && dx_row_stride >= n &&
+                   (!dres || dres_row_stride >= n) && (!ddelta || ddelta_row_stride >= n),
+               "%s: row stride < n", what);
+  return PB_OK;
+}
+}  // namespace
+}  // namespace pb
+
+extern "C" int pb_add_rmsnorm_bwd(const void *dy, int64_t dy_row_stride, int dy_dtype,
+                                  const void *h, int64_t h_row_stride, int h_dtype, const void *w,
+                                  int w_dtype, const float *rstd, const void *dres,
+                                  int64_t dres_row_stride, void *dx, int64_t dx_row_stride,
+                                  void *ddelta, int64_t ddelta_row_stride, int ddelta_dtype,
+                                  void *dw, int dw_accumulate, void *workspace, int64_t rows,
+                                  int64_t n, void *stream) {
+  using namespace pb;
+  clear_error();
+  int rc = check_bwd_args("pb_add_rmsnorm_bwd", dy_dtype, h_dtype, w_dtype, ddelta, ddelta_dtype,
+                          rows, n, dy_row_stride, h_row_stride, dx_row_stride, dres,
+                          dres_row_stride, ddelta_row_stride);
+  if (rc) return rc;
+  PB_CHECK_ARG(w && dw, "pb_add_rmsnorm_bwd: null weight or dw");
+  PB_CHECK_ARG(!dw_accumulate || w_dtype == PB_F32,
+               "pb_add_rmsnorm_bwd: dw_accumulate needs an fp32 weight (and dw)");
+  hipStream_t st = as_stream(stream);
+  if (rows == 0) {
+    if (!dw_accumulate)
+      hipLaunchKernelGGL(add_rmsnorm_dw_zero, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                         static_cast<char *>(dw), w_dtype, (int)n);
+    return launch_status("pb_add_rmsnorm_bwd(empty)");
+  }
+  PB_CHECK_ARG(dy && h && rstd && dx, "pb_add_rmsnorm_bwd: null argument");
+  PB_CHECK_ARG(workspace != nullptr, "pb_add_rmsnorm_bwd: workspace is required");
+  const int nwg = add_rmsnorm_bwd_rows(dy, dy_row_stride, dy_dtype, h, h_row_stride, h_dtype, w,
+                                       w_dtype, rstd, dres, dres_row_stride, dx, dx_row_stride,
+                                       ddelta, ddelta_row_stride, ddelta_dtype, workspace, rows, n,
+                                       st, "pb_add_rmsnorm_bwd");
+  if (nwg < 0) return -nwg;
   hipLaunchKernelGGL(add_rmsnorm_dw_reduce, dim3((unsigned)((n + 63) / 64)), dim3(64 * kRedWaves),
-                     0, st, a.partial, static_cast<char *>(dw), w_dtype, nwg, (int)n,
-                     dw_accumulate ? 1 : 0);
+                     0, st, static_cast<const float *>(workspace), static_cast<char *>(dw), w_dtype,
+                     nwg, (int)n, dw_accumulate ? 1 : 0);
   return launch_status("pb_add_rmsnorm_bwd(dw)");
+}
+
+extern "C" int pb_add_rmsnorm_bwd_partials(const void *dy, int64_t dy_row_stride, int dy_dtype,
+                                           const void *h, int64_t h_row_stride, int h_dtype,
+                                           const void *w, int w_dtype, const float *rstd,
+                                           const void *dres, int64_t dres_row_stride, void *dx,
+                                           int64_t dx_row_stride, void *ddelta,
+                                           int64_t ddelta_row_stride, int ddelta_dtype,
+                                           float *partials, int64_t rows, int64_t n,
+                                           void *stream) {
+  using namespace pb;
+  clear_error();
+  int rc = check_bwd_args("pb_add_rmsnorm_bwd_partials", dy_dtype, h_dtype, w_dtype, ddelta,
+                          ddelta_dtype, rows, n, dy_row_stride, h_row_stride, dx_row_stride, dres,
+                          dres_row_stride, ddelta_row_stride);
+  if (rc) return rc;
+  if (rows == 0) return PB_OK;  // no partial rows: the reduction adds nothing
+  PB_CHECK_ARG(dy && h && w && rstd && dx && partials, "pb_add_rmsnorm_bwd_partials: null argument");
+  const int nwg = add_rmsnorm_bwd_rows(dy, dy_row_stride, dy_dtype, h, h_row_stride, h_dtype, w,
+                                       w_dtype, rstd, dres, dres_row_stride, dx, dx_row_stride,
+                                       ddelta, ddelta_row_stride, ddelta_dtype, partials, rows, n,
+                                       as_stream(stream), "pb_add_rmsnorm_bwd_partials");
+  return nwg < 0 ? -nwg : PB_OK;
+}
+
+extern "C" int pb_rmsnorm_dw_reduce_batched(const float *partials, int64_t problem_stride,
+                                            float *const *dw, int64_t count, int64_t rows,
+                                            int64_t n, void *stream) {
+  using namespace pb;
+  clear_error();
+  PB_CHECK_ARG(count >= 0 && rows >= 0 && n > 0 && n <= 65536,
+               "pb_rmsnorm_dw_reduce_batched: bad shape count=%lld rows=%lld n=%lld",
+               (long long)count, (long long)rows, (long long)n);
+  if (count == 0 || rows == 0) return PB_OK;
+  int rpw;
+  const int nparts = bwd_nwg(rows, rpw);
+  PB_CHECK_ARG(partials && dw && problem_stride >= (int64_t)nparts * n,
+               "pb_rmsnorm_dw_reduce_batched: null argument or problem stride < partial table");
+  hipStream_t st = as_stream(stream);
+  for (int64_t i0 = 0; i0 < count; i0 += kDwBatch) {
+    const int m = (int)std::min<int64_t>(kDwBatch, count - i0);
+    DwBatch b{};
+    for (int i = 0; i < m; ++i) {
+      PB_CHECK_ARG(dw[i0 + i] != nullptr, "pb_rmsnorm_dw_reduce_batched: null dw[%lld]",
+                   (long long)(i0 + i));
+      b.dw[i] = dw[i0 + i];
+    }
+    hipLaunchKernelGGL(rmsnorm_dw_reduce_batched, dim3((unsigned)((n + 63) / 64), (unsigned)m),
+                       dim3(64 * kRedWaves), 0, st, partials + i0 * problem_stride, problem_stride,
+                       b, nparts, (int)n);
+    const int s = launch_status("pb_rmsnorm_dw_reduce_batched");
+    if (s) return s;
+  }
+  return PB_OK;
 }

@@ -13,6 +13,8 @@ Unlike the reference there is no CPU fallback: CPU tensors raise.
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from packbalance_amd import _native as N
@@ -117,6 +119,37 @@ def _bwd_call(dy2d, h2d, w, rstd, dres, dx, ddelta, dw, accumulate=False):
     )
 
 
+def _bwd_partials_call(dy2d, h2d, w, rstd, dres, dx, ddelta, partials):
+    """The backward without its dw reduction: the per-workgroup fp32 dw partials go
+    to ``partials`` (``pb_add_rmsnorm_bwd_workspace_bytes`` bytes) for a later
+    batched reduction (``pb_rmsnorm_dw_reduce_batched``)."""
+    rows, n = h2d.shape
+    N.call(
+        "pb_add_rmsnorm_bwd_partials",
+        dy2d.data_ptr(), dy2d.stride(0), N.dtype_code(dy2d),
+        h2d.data_ptr(), h2d.stride(0), N.dtype_code(h2d),
+        w.data_ptr(), N.dtype_code(w), rstd.data_ptr(),
+        dres.data_ptr() if dres is not None else None, dres.stride(0) if dres is not None else n,
+        dx.data_ptr(), dx.stride(0),
+        ddelta.data_ptr() if ddelta is not None else None,
+        ddelta.stride(0) if ddelta is not None else n,
+        N.dtype_code(ddelta) if ddelta is not None else N.dtype_code(dx),
+        partials.data_ptr(), rows, n, N.stream_ptr(h2d),
+    )
+
+
+def partial_floats(rows: int, n: int) -> int:
+    """fp32 elements of one norm backward's dw partial table."""
+    return N.lib().pb_add_rmsnorm_bwd_workspace_bytes(rows, n) // 4
+
+
+def dw_reduce_batched(partials: torch.Tensor, dws: list, rows: int, n: int) -> None:
+    """dws[i] (fp32 [n]) += the column sums of partials[i] ([count, >= partial_floats])."""
+    ptrs = (ctypes.c_void_p * len(dws))(*[g.data_ptr() for g in dws])
+    N.call("pb_rmsnorm_dw_reduce_batched", partials.data_ptr(), partials.stride(0), ptrs,
+           len(dws), rows, n, N.stream_ptr(partials))
+
+
 def _check_acc(dw_acc, weight):
     if dw_acc is None:
         return
@@ -145,7 +178,7 @@ def _out_buffer(buf, rows, n, dtype, device, what):
 
 class _AddRMSNorm(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, delta, weight, eps, out_dtype, dw_acc, y_out, ddelta_out):
+    def forward(ctx, x, delta, weight, eps, out_dtype, dw_acc, y_out, ddelta_out, dw_defer):
         _check(x, weight, "add_rmsnorm")
         _check_acc(dw_acc, weight)
         if delta.shape != x.shape:
@@ -161,6 +194,7 @@ class _AddRMSNorm(torch.autograd.Function):
         ctx.save_for_backward(h, w, rstd)
         ctx.meta = (x.shape, delta.dtype, weight.dtype)
         ctx.dw_acc = dw_acc
+        ctx.dw_defer = dw_defer if dw_acc is not None else None
         ctx.ddelta_out = ddelta_out
         return h.reshape(x.shape), y.reshape(x.shape)
 
@@ -176,20 +210,27 @@ class _AddRMSNorm(torch.autograd.Function):
             dres = dres if dres.dtype == h.dtype else dres.to(h.dtype)
         dx = torch.empty_like(h)
         ddelta = _out_buffer(ctx.ddelta_out, rows, n, delta_dtype, h.device, "add_rmsnorm")
+        if ctx.dw_defer is not None:
+            plan, slot = ctx.dw_defer
+            _bwd_partials_call(dy2d, h, w, rstd, dres, dx, ddelta, plan.norm_partials(slot))
+            plan.add_norm(slot, ctx.dw_acc)
+            return (dx.reshape(shape), ddelta.reshape(shape), None, None, None, None, None, None,
+                    None)
         if ctx.dw_acc is not None:
             _bwd_call(dy2d, h, w, rstd, dres, dx, ddelta, ctx.dw_acc, accumulate=True)
-            return dx.reshape(shape), ddelta.reshape(shape), None, None, None, None, None, None
+            return (dx.reshape(shape), ddelta.reshape(shape), None, None, None, None, None, None,
+                    None)
         dw = torch.empty(n, dtype=w.dtype, device=w.device)
         _bwd_call(dy2d, h, w, rstd, dres, dx, ddelta, dw)
         return (dx.reshape(shape), ddelta.reshape(shape), dw.to(w_dtype), None, None, None, None,
-                None)
+                None, None)
 
 
 class _RMSNormTo(torch.autograd.Function):
     """RMSNorm whose output dtype differs from the input's (no residual add)."""
 
     @staticmethod
-    def forward(ctx, x, weight, eps, out_dtype, dw_acc, y_out):
+    def forward(ctx, x, weight, eps, out_dtype, dw_acc, y_out, dw_defer):
         _check(x, weight, "rmsnorm")
         _check_acc(dw_acc, weight)
         x2d, w = _rows(x), weight.contiguous()
@@ -200,6 +241,7 @@ class _RMSNormTo(torch.autograd.Function):
         ctx.save_for_backward(x2d, w, rstd)
         ctx.meta = (x.shape, weight.dtype)
         ctx.dw_acc = dw_acc
+        ctx.dw_defer = dw_defer if dw_acc is not None else None
         return y.reshape(x.shape)
 
     @staticmethod
@@ -207,17 +249,23 @@ class _RMSNormTo(torch.autograd.Function):
         x2d, w, rstd = ctx.saved_tensors
         shape, w_dtype = ctx.meta
         dx = torch.empty_like(x2d)
+        if ctx.dw_defer is not None:
+            plan, slot = ctx.dw_defer
+            _bwd_partials_call(_rows(dy), x2d, w, rstd, None, dx, None, plan.norm_partials(slot))
+            plan.add_norm(slot, ctx.dw_acc)
+            return dx.reshape(shape), None, None, None, None, None, None
         if ctx.dw_acc is not None:
             _bwd_call(_rows(dy), x2d, w, rstd, None, dx, None, ctx.dw_acc, accumulate=True)
-            return dx.reshape(shape), None, None, None, None, None
+            return dx.reshape(shape), None, None, None, None, None, None
         dw = torch.empty(x2d.shape[1], dtype=w.dtype, device=w.device)
         _bwd_call(_rows(dy), x2d, w, rstd, None, dx, None, dw)
-        return dx.reshape(shape), dw.to(w_dtype), None, None, None, None
+        return dx.reshape(shape), dw.to(w_dtype), None, None, None, None, None
 
 
 def add_rmsnorm(x: torch.Tensor, delta: torch.Tensor, weight: torch.Tensor, eps: float,
                 out_dtype: torch.dtype | None = None, dw_acc: torch.Tensor | None = None,
-                y_out: torch.Tensor | None = None, ddelta_out: torch.Tensor | None = None):
+                y_out: torch.Tensor | None = None, ddelta_out: torch.Tensor | None = None,
+                dw_defer=None):
     """Residual add fused with the next RMSNorm (gfx950 kernel).
 
     Returns ``(h, y)``: ``h = x + delta`` in x's dtype (the new residual stream) and
@@ -228,17 +276,20 @@ def add_rmsnorm(x: torch.Tensor, delta: torch.Tensor, weight: torch.Tensor, eps:
     ``dw_acc`` by the backward kernel and the gradient returned for ``weight`` is None.
     ``y_out`` / ``ddelta_out`` (contiguous [rows, n] buffers) receive y and the
     backward's ddelta instead of new tensors (the decoder's batched weight-gradient
-    plan hands out its slots this way).
+    plan hands out its slots this way).  ``dw_defer = (plan, slot)`` (with ``dw_acc``)
+    leaves the backward's dw partials in ``plan.norm_partials(slot)`` and registers
+    ``dw_acc`` with ``plan.add_norm``: the plan reduces every deferred norm of the
+    pass in one launch when the backward ends (same bits as the immediate sum).
     """
     return _AddRMSNorm.apply(x, delta, weight, eps, out_dtype or x.dtype, dw_acc, y_out,
-                             ddelta_out)
+                             ddelta_out, dw_defer)
 
 
 def rmsnorm_to(x: torch.Tensor, weight: torch.Tensor, eps: float,
                out_dtype: torch.dtype, dw_acc: torch.Tensor | None = None,
-               y_out: torch.Tensor | None = None) -> torch.Tensor:
+               y_out: torch.Tensor | None = None, dw_defer=None) -> torch.Tensor:
     """``rmsnorm`` written directly in ``out_dtype`` (e.g. fp32 residual -> bf16 activations);
-    ``dw_acc`` and ``y_out`` as for ``add_rmsnorm``."""
+    ``dw_acc``, ``y_out`` and ``dw_defer`` as for ``add_rmsnorm``."""
     if out_dtype == x.dtype and dw_acc is None and y_out is None:
         return rmsnorm(x, weight, eps)
-    return _RMSNormTo.apply(x, weight, eps, out_dtype, dw_acc, y_out)
+    return _RMSNormTo.apply(x, weight, eps, out_dtype, dw_acc, y_out, dw_defer)

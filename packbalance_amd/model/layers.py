@@ -162,9 +162,10 @@ class WgradPlan:
     """
 
     batched_gemms = 0  # batched GEMMs issued by all plans (a host-side counter)
+    norm_reduces = 0  # batched norm dw reductions issued by all plans
 
     def __init__(self, n_layers: int, tokens: int, dims: dict, dtype: torch.dtype,
-                 device: torch.device) -> None:
+                 device: torch.device, norms: int = 0, norm_dim: int = 0) -> None:
         self.L, self.T = n_layers, tokens
         self.dims = dict(dims)
         self.x = {k: torch.empty((n_layers, tokens, c), dtype=dtype, device=device)
@@ -172,6 +173,18 @@ class WgradPlan:
         self.dy = {k: torch.empty((n_layers, tokens, r), dtype=dtype, device=device)
                    for k, (r, _) in self.dims.items()}
         self.g = {k: [None] * n_layers for k in self.dims}
+        # RMSNorm weight gradients (``norms`` norms over [tokens, norm_dim] rows): each
+        # norm's backward leaves its per-workgroup dw partials in its row here, and
+        # the pass's end adds all of them to their fp32 targets in one launch
+        # (at cfg2: 25 small reduction launches per micro-batch -> 1).
+        self.norm_dim = norm_dim
+        self.norm_parts = None
+        if norms:
+            from packbalance_amd.kernels.rmsnorm import partial_floats
+
+            self.norm_parts = torch.empty((norms, max(1, partial_floats(tokens, norm_dim))),
+                                          dtype=torch.float32, device=device)
+        self.norm_g = [None] * norms
         self._task = None
 
     def x_of(self, kind: str, layer: int) -> torch.Tensor:
@@ -196,6 +209,19 @@ class WgradPlan:
     def add(self, kind: str, layer: int, g: torch.Tensor) -> None:
         """Called from a layer's backward once ``dy_of(kind, layer)`` holds its dy."""
         self.g[kind][layer] = g
+        self._queue_flush()
+
+    def norm_partials(self, slot: int) -> torch.Tensor:
+        """Norm ``slot``'s dw partial table (filled by its backward)."""
+        return self.norm_parts[slot]
+
+    def add_norm(self, slot: int, g: torch.Tensor) -> None:
+        """Called from a norm's backward once ``norm_partials(slot)`` holds its partials;
+        ``g`` (fp32 [norm_dim]) receives their sum when the pass ends."""
+        self.norm_g[slot] = g
+        self._queue_flush()
+
+    def _queue_flush(self) -> None:
         task = torch._C._current_graph_task_id()
         if task != self._task:
             self._task = task
@@ -218,8 +244,25 @@ class WgradPlan:
                 return None
         return g0.as_strided((self.L, r, c), (stride, c, 1))
 
+    def _flush_norms(self) -> None:
+        from packbalance_amd.kernels.rmsnorm import dw_reduce_batched
+
+        i, n = 0, len(self.norm_g)
+        while i < n:  # runs of consecutive registered slots, one launch each
+            if self.norm_g[i] is None:
+                i += 1
+                continue
+            j = i
+            while j < n and self.norm_g[j] is not None:
+                j += 1
+            dw_reduce_batched(self.norm_parts[i:j], self.norm_g[i:j], self.T, self.norm_dim)
+            WgradPlan.norm_reduces += 1
+            i = j
+        self.norm_g = [None] * n
+
     def flush(self) -> None:
         self._task = None
+        self._flush_norms()
         for kind in self.dims:
             if all(g is None for g in self.g[kind]):
                 continue

@@ -179,16 +179,21 @@ class LlamaDecoderLayer(nn.Module):
         none = lambda kind, i: None  # noqa: E731
         x_slot = none if plan is None else plan.x_of
         dy_slot = none if plan is None else plan.dy_of
+        # Norm weight gradients: reduced by the plan at the end of the backward
+        # (norm slots 2 layer and 2 layer + 1; the final norm takes 2 L).
+        defer = (lambda i: None) if plan is None else (lambda i: (plan, i))  # noqa: E731
         if pending is None:
             x = rmsnorm_to(hidden, w1, eps, dt, dw_acc=flat.grad_of([w1]),
-                           y_out=x_slot("qkv", layer))
+                           y_out=x_slot("qkv", layer), dw_defer=defer(2 * layer))
         else:
             hidden, x = add_rmsnorm(hidden, pending, w1, eps, dt, dw_acc=flat.grad_of([w1]),
                                     y_out=x_slot("qkv", layer),
-                                    ddelta_out=dy_slot("down", layer - 1))
+                                    ddelta_out=dy_slot("down", layer - 1),
+                                    dw_defer=defer(2 * layer))
         a = self.self_attn.fused(x, cos, sin, doc_ids, block_mask, flat, dt, wt, plan, layer)
         hidden, x = add_rmsnorm(hidden, a, w2, eps, dt, dw_acc=flat.grad_of([w2]),
-                                y_out=x_slot("gate_up", layer), ddelta_out=dy_slot("o", layer))
+                                y_out=x_slot("gate_up", layer), ddelta_out=dy_slot("o", layer),
+                                dw_defer=defer(2 * layer + 1))
         return hidden, self.mlp.fused(x, flat, dt, wt, plan, layer)
 
 
@@ -255,7 +260,8 @@ class LlamaForCausalLM(nn.Module):
         nq, nkv = c.n_heads * c.head_dim, c.n_kv_heads * c.head_dim
         dims = {"qkv": (nq + 2 * nkv, c.d_model), "o": (c.d_model, nq),
                 "gate_up": (2 * c.d_ff, c.d_model), "down": (c.d_model, c.d_ff)}
-        return L.WgradPlan(len(self.layers), tokens, dims, dt, dev)
+        return L.WgradPlan(len(self.layers), tokens, dims, dt, dev,
+                           norms=2 * len(self.layers) + 1, norm_dim=c.d_model)
 
     def prepare(self, dt: torch.dtype) -> None:
         """Build the weight copies that forwards share (compute copy, transposed
@@ -290,7 +296,8 @@ class LlamaForCausalLM(nn.Module):
             _, y = add_rmsnorm(hidden, pending, self.norm.weight, self.norm.eps, dt,
                                dw_acc=flat.grad_of([self.norm.weight]),
                                ddelta_out=None if plan is None else plan.dy_of(
-                                   "down", len(self.layers) - 1))
+                                   "down", len(self.layers) - 1),
+                               dw_defer=None if plan is None else (plan, 2 * len(self.layers)))
             kw = dict(ignore_index=-100, z_loss_coeff=self.cfg.z_loss_coeff)
             if dt == torch.float32 or self.cfg.d_model % 8:
                 return linear_cross_entropy(y, self.embed_tokens.weight, labels,

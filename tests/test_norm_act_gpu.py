@@ -300,3 +300,45 @@ def test_norm_weight_grad_accumulates_into_fp32_buffer(rows, n, dev) -> None:
         torch.testing.assert_close(acc - acc0, wr.grad, rtol=1e-5, atol=1e-4)
     with pytest.raises(ValueError):
         add_rmsnorm(x, d, w.to(torch.bfloat16), 1e-5, dw_acc=acc0)
+
+
+def test_norm_weight_grad_deferred_to_a_batched_reduce(dev) -> None:
+    """dw_defer: 35 norms of one backward pass (slot 0 an rmsnorm_to, the rest
+    add_rmsnorm; slot 5 unused) leave their dw partials in a WgradPlan, which adds
+    them to their fp32 buffers when the pass ends, in two runs of consecutive
+    slots (the second, 30 norms, plus the first's 5, launched as 32-problem
+    batches); every buffer and dx equal the immediate dw_acc path bit for bit."""
+    from packbalance_amd.kernels.rmsnorm import add_rmsnorm, rmsnorm_to
+    from packbalance_amd.model.layers import WgradPlan
+
+    rows, n, count = 4096, 768, 36
+    g = torch.Generator().manual_seed(11)
+    xs = [torch.randn(rows, n, generator=g).to(dev) for _ in range(count)]
+    ds = [torch.randn(rows, n, generator=g).to(dev, torch.bfloat16) for _ in range(count)]
+    ws = [(torch.randn(n, generator=g) * 0.1 + 1.0).to(dev) for _ in range(count)]
+    dys = [torch.randn(rows, n, generator=g).to(dev, torch.bfloat16) for _ in range(count)]
+    acc0 = torch.randn(count, n, generator=g).to(dev)
+    slots = [i for i in range(count) if i != 5]
+    plan = WgradPlan(1, rows, {}, torch.bfloat16, dev, norms=count, norm_dim=n)
+
+    def run(defer):
+        acc = acc0.clone()
+        xr = [x.clone().requires_grad_(True) for x in xs]
+        outs = []
+        for i in slots:
+            kw = dict(dw_acc=acc[i], dw_defer=(plan, i) if defer else None)
+            if i == 0:
+                outs.append(rmsnorm_to(xr[i], ws[i], 1e-5, torch.bfloat16, **kw))
+            else:
+                outs.append(add_rmsnorm(xr[i], ds[i], ws[i], 1e-5, torch.bfloat16, **kw)[1])
+        torch.autograd.backward(outs, [dys[i] for i in slots])
+        return acc, [xr[i].grad for i in slots]
+
+    before = WgradPlan.norm_reduces
+    acc_d, dx_d = run(True)
+    assert WgradPlan.norm_reduces - before == 2
+    acc_i, dx_i = run(False)
+    assert torch.equal(acc_d, acc_i)
+    assert torch.equal(acc_d[5], acc0[5])
+    assert all(torch.equal(a, b) for a, b in zip(dx_d, dx_i))
+    assert not torch.equal(acc_d, acc0)
