@@ -178,6 +178,7 @@ def train_step_bench(steps: int, warmup: int, dev, use_graph: bool = True, strea
         "packs_built_on_device": True,
         "micro_batch_streams": len(ts.streams) or 1,
         "packs_per_micro_batch": ts.k,
+        "lm_head_logits_kept": ts.keep_logits_bytes >= cfg.vocab_size * ts.k * 2048 * 2,
     }
     # The first timed step's 4 packs, on the host, for the CPU baseline.
     first = build_pack_batch(store, step_packs[warmup], 2048)
@@ -688,6 +689,7 @@ def main() -> int:
             "hip_graph": train["hip_graph"],
             "micro_batch_streams": train["micro_batch_streams"],
             "packs_per_micro_batch": train["packs_per_micro_batch"],
+            "lm_head_logits_kept": train["lm_head_logits_kept"],
         },
         "masked_attn_tflops": kernels.get("attention", {}).get("fwd_bwd_tflops"),
         "ce_gbps": kernels.get("ce_rows", {}).get("gbps"),

@@ -120,9 +120,9 @@ def test_concurrent_micro_batches_match_sequential(dev) -> None:
 
 
 def test_kept_logits_step_matches_recomputing_step(dev) -> None:
-    """``keep_logits_bytes``: the LM-head forward keeps its bf16 logits and the
-    backward forms dlogits from them instead of recomputing the logits GEMM.
-    The same numerics as the default step: step 0's loss is identical (same
+    """``keep_logits_bytes`` (the step's default): the LM-head forward keeps its
+    bf16 logits and the backward forms dlogits from them instead of recomputing
+    the logits GEMM.  The same numerics as the recomputing step (0 bytes): step 0's loss is identical (same
     forward) and its gradient agrees to 1e-4 of its largest entry (the backward
     GEMM may round a logit's fp32 sum to the neighbouring bf16 value); later
     eager steps, and graph replays of the kept-logits step, are held to the
@@ -133,7 +133,7 @@ def test_kept_logits_step_matches_recomputing_step(dev) -> None:
     with logits_budget(1 << 30):
         assert stores_logits(2 * 256, cfg.vocab_size)  # the path under test is taken
     store, _, tables = _store_tables(cfg, dev, seed=3, n_steps=4)
-    ref = TrainStep(cfg, dev, seq_len=256, store=store, streams=2)
+    ref = TrainStep(cfg, dev, seq_len=256, store=store, streams=2, keep_logits_bytes=0)
     kept = TrainStep(cfg, dev, seq_len=256, store=store, streams=2, keep_logits_bytes=1 << 30)
     for i, packs in enumerate(tables):
         ref.eager_packs(packs)
@@ -148,7 +148,7 @@ def test_kept_logits_step_matches_recomputing_step(dev) -> None:
         assert abs(lr_ - lk) <= 1e-3 * abs(lr_), (i, lr_, lk)
         assert abs(nr - nk) <= 1e-3 * abs(nr) + 1e-6, (i, nr, nk)
 
-    eager = TrainStep(cfg, dev, seq_len=256, store=store)
+    eager = TrainStep(cfg, dev, seq_len=256, store=store, keep_logits_bytes=0)
     graph = TrainStep(cfg, dev, seq_len=256, store=store, streams=2, keep_logits_bytes=1 << 30)
     graph.capture_packs(tables[0])
     for _ in range(2):
