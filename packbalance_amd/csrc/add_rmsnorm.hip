@@ -457,8 +457,8 @@ extern "C" int64_t pb_add_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t n) {
 namespace pb {
 namespace {
 // The backward kernel alone: dx, ddelta and the dw partials [nwg, n] in
-// `workspace` (arguments checked by the caller, rows > 0).  Returns nwg or
-// a negative status.
+// `workspace` (arguments checked by the caller, rows > 0).  Returns nwg, or
+// the (negative) launch status on failure.
 int add_rmsnorm_bwd_rows(const void *dy, int64_t dy_row_stride, int dy_dtype, const void *h,
                          int64_t h_row_stride, int h_dtype, const void *w, int w_dtype,
                          const float *rstd, const void *dres, int64_t dres_row_stride, void *dx,
@@ -495,7 +495,7 @@ int add_rmsnorm_bwd_rows(const void *dy, int64_t dy_row_stride, int dy_dtype, co
     default: hipLaunchKernelGGL(add_rmsnorm_bwd_loop, grid, dim3(kThreads), 0, st, a);
   }
   const int s = launch_status(what);
-  return s ? -s : nwg;
+  return s < 0 ? s : nwg;
 }
 
 int check_bwd_args(const char *what, int dy_dtype, int h_dtype, int w_dtype, const void *ddelta,
@@ -544,7 +544,7 @@ extern "C" int pb_add_rmsnorm_bwd(const void *dy, int64_t dy_row_stride, int dy_
                                        w_dtype, rstd, dres, dres_row_stride, dx, dx_row_stride,
                                        ddelta, ddelta_row_stride, ddelta_dtype, workspace, rows, n,
                                        st, "pb_add_rmsnorm_bwd");
-  if (nwg < 0) return -nwg;
+  if (nwg < 0) return nwg;
   hipLaunchKernelGGL(add_rmsnorm_dw_reduce, dim3((unsigned)((n + 63) / 64)), dim3(64 * kRedWaves),
                      0, st, static_cast<const float *>(workspace), static_cast<char *>(dw), w_dtype,
                      nwg, (int)n, dw_accumulate ? 1 : 0);
@@ -571,7 +571,7 @@ extern "C" int pb_add_rmsnorm_bwd_partials(const void *dy, int64_t dy_row_stride
                                        w_dtype, rstd, dres, dres_row_stride, dx, dx_row_stride,
                                        ddelta, ddelta_row_stride, ddelta_dtype, partials, rows, n,
                                        as_stream(stream), "pb_add_rmsnorm_bwd_partials");
-  return nwg < 0 ? -nwg : PB_OK;
+  return nwg < 0 ? nwg : PB_OK;
 }
 
 extern "C" int pb_rmsnorm_dw_reduce_batched(const float *partials, int64_t problem_stride,
