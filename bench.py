@@ -424,6 +424,8 @@ def lmhead_ce_kernels(dev, iters: int, vchunk: int = 8192, stored: bool = False)
                  "pass; 6NVD executed and counted" if kept else
                  "no full logits (cfg4's rule): fwd 2NVD + bwd 6NVD executed (logits "
                  "recomputed once); 6NVD counted"),
+        "kernels": ("lse and dlogits on this build's MFMA kernels (pb_lmhead_ce_fwd, "
+                    "pb_lmhead_ce_dlogits); dx and dW as plain hipBLASLt GEMMs (torch)"),
     }
 
 

@@ -303,6 +303,22 @@ int pb_lmhead_ce_bwd_logits(const void *x, int64_t ldx, const void *w, int64_t l
                             int dw_accumulate, int logits_dtype, const void *logits,
                             int64_t ldlg, void *stream);
 
+/* One vocab chunk of the backward's dlogits (no reference counterpart: the
+ * dL step of pb_lmhead_ce_bwd / _logits, fused_ce.py:176-202, for callers
+ * that run the dx and dW products on a GEMM library -- the Python layer runs
+ * them through torch on hipBLASLt):
+ *   dL [n][vc] (row stride ldl) and dL^T [vc][n] (row stride ldlt), bf16,
+ *   of vocab rows v0 .. v0 + vc - 1 (v0 + vc <= v),
+ * from the stored logits^T of pb_lmhead_ce_fwd_logits (logits != NULL, its
+ * logits_dtype) or by recomputing them (rounded to bf16 for PB_BF16), with
+ * the lse of the forward and grad_out a device pointer to one fp32.  x, w,
+ * dl and dlt 16-byte aligned with row strides % 8 == 0, d % 8 == 0.        */
+int pb_lmhead_ce_dlogits(const void *x, int64_t ldx, const void *w, int64_t ldw, int64_t n,
+                         int64_t v, int64_t d, const int64_t *targets, int64_t ignore_index,
+                         float z_loss_coeff, const float *lse, const float *grad_out,
+                         int64_t v0, int64_t vc, void *dl, int64_t ldl, void *dlt, int64_t ldlt,
+                         int logits_dtype, const void *logits, int64_t ldlg, void *stream);
+
 /* ---- Fused residual add + RMSNorm (per-operand dtypes) ------------------
  * Replaces the decoder's `hidden = hidden + sublayer_out` followed by the
  * next rmsnorm (packbalance/model/llama.py:122-125 with

@@ -116,6 +116,11 @@ SIGNATURES: dict[str, tuple] = {
         [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _p, _i64, _f32, _p, _p,
          _i64, _p, _p, _i32, _i64, _p, _i32, _i64, _i32, _i32, _p, _i64, _p],
     ),
+    "pb_lmhead_ce_dlogits": (
+        _i32,
+        [_p, _i64, _p, _i64, _i64, _i64, _i64, _p, _i64, _f32, _p, _p, _i64, _i64, _p, _i64, _p,
+         _i64, _i32, _p, _i64, _p],
+    ),
     "pb_pack_bf16": (_i32, [_p, _i32, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i32, _p]),
     "pb_add_rmsnorm_fwd": (
         _i32,

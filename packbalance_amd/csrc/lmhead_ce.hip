@@ -1043,6 +1043,60 @@ extern "C" int64_t pb_lmhead_ce_bwd_workspace_bytes(int64_t n, int64_t v, int64_
 }
 
 namespace {
+// dL [n][vc] (row stride ldl) and dL^T [vc][ldlt] of vocab rows v0 .. v0 + vc:
+// from the stored logits^T when given, else by the recomputing GEMM.
+int dlogits_chunk(const void *x, int64_t ldx, const void *w, int64_t ldw, int64_t n, int64_t v,
+                  int64_t d, const int64_t *targets, int64_t ignore_index, float z_loss_coeff,
+                  const float *lse, const float *grad_out, int64_t v0, int vc, pb::bf16_t *dl,
+                  int64_t ldl, pb::bf16_t *dlt, int64_t ldlt, bool round_bf16, const void *logits,
+                  int64_t ldlg, hipStream_t st) {
+  using namespace pb;
+  using namespace pb::ce;
+  if (logits) {
+    DlArgs da = {};
+    da.lg = static_cast<const bf16_t *>(logits);
+    da.ldlg = ldlg;
+    da.v0 = (int)v0; da.vc = vc; da.n = (int)n;
+    da.targets = targets;
+    da.ignore_index = ignore_index;
+    da.z = z_loss_coeff;
+    da.lse = lse;
+    da.grad_out = grad_out;
+    da.dl = dl; da.dlt = dlt;
+    da.ldl = ldl; da.ldlt = ldlt;
+    const dim3 grid((unsigned)((vc + kDlRows - 1) / kDlRows),
+                    (unsigned)((n + kDlTokens - 1) / kDlTokens));
+    if (round_bf16)
+      hipLaunchKernelGGL(dlogits_stored<bf16_t>, grid, dim3(256), 0, st, da);
+    else
+      hipLaunchKernelGGL(dlogits_stored<float>, grid, dim3(256), 0, st, da);
+    return launch_status("pb_lmhead_ce(dlogits)");
+  }
+  GemmArgs g = {};
+  g.A = static_cast<const bf16_t *>(w) + v0 * ldw;
+  g.lda = ldw;
+  g.B = static_cast<const bf16_t *>(x);
+  g.ldb = ldx;
+  g.M = vc; g.N = (int)n; g.K = (int)d;
+  g.v0 = (int)v0; g.V = (int)v;
+  g.targets = targets;
+  g.ignore_index = ignore_index;
+  g.z = z_loss_coeff;
+  g.lse = lse;
+  g.grad_out = grad_out;
+  g.dl = dl;
+  g.dlt = dlt;
+  g.ldl = ldl;
+  g.ldlt = ldlt;
+  g.round_bf16 = round_bf16;
+  if (dma_ok(d))
+    hipLaunchKernelGGL((gemm_nt_dma<kDlogits, RowShape>), dim3(dma_tiles<RowShape>(g.M, g.N)),
+                       dim3(RowShape::NT), 0, st, g);
+  else
+    hipLaunchKernelGGL(gemm_nt<kDlogits>, dim3(tiles(g.M, g.N)), dim3(256), 0, st, g);
+  return launch_status("pb_lmhead_ce(dlogits)");
+}
+
 int lmhead_bwd(const void *x, int64_t ldx, const void *w, int64_t ldw, const void *xt,
                int64_t ldxt, const void *wt, int64_t ldwt, int64_t n, int64_t v, int64_t d,
                const int64_t *targets, int64_t ignore_index, float z_loss_coeff,
@@ -1078,51 +1132,8 @@ int lmhead_bwd(const void *x, int64_t ldx, const void *w, int64_t ldw, const voi
     const int vc = (int)((v - v0) < vchunk ? (v - v0) : vchunk);
     // 1) dlogits for vocab rows [v0, v0 + vc): dL [n][vc], dL^T [vc][n] --
     // from the stored logits, or by recomputing them.
-    if (logits) {
-      DlArgs da = {};
-      da.lg = static_cast<const bf16_t *>(logits);
-      da.ldlg = ldlg;
-      da.v0 = (int)v0; da.vc = vc; da.n = (int)n;
-      da.targets = targets;
-      da.ignore_index = ignore_index;
-      da.z = z_loss_coeff;
-      da.lse = lse;
-      da.grad_out = grad_out;
-      da.dl = dl; da.dlt = dlt;
-      da.ldl = ldl; da.ldlt = ldlt;
-      const dim3 grid((unsigned)((vc + kDlRows - 1) / kDlRows),
-                      (unsigned)((n + kDlTokens - 1) / kDlTokens));
-      if (round_bf16)
-        hipLaunchKernelGGL(dlogits_stored<bf16_t>, grid, dim3(256), 0, st, da);
-      else
-        hipLaunchKernelGGL(dlogits_stored<float>, grid, dim3(256), 0, st, da);
-    }
-    GemmArgs g = {};
-    g.A = static_cast<const bf16_t *>(w) + v0 * ldw;
-    g.lda = ldw;
-    g.B = static_cast<const bf16_t *>(x);
-    g.ldb = ldx;
-    g.M = vc; g.N = (int)n; g.K = (int)d;
-    g.v0 = (int)v0; g.V = (int)v;
-    g.targets = targets;
-    g.ignore_index = ignore_index;
-    g.z = z_loss_coeff;
-    g.lse = lse;
-    g.grad_out = grad_out;
-    g.dl = dl;
-    g.dlt = dlt;
-    g.ldl = ldl;
-    g.ldlt = ldlt;
-    g.round_bf16 = round_bf16;
-    if (logits) {
-      // dL, dL^T written above
-    } else if (dma_ok(d)) {
-      hipLaunchKernelGGL((gemm_nt_dma<kDlogits, RowShape>), dim3(dma_tiles<RowShape>(g.M, g.N)),
-                         dim3(RowShape::NT), 0, st, g);
-    } else {
-      hipLaunchKernelGGL(gemm_nt<kDlogits>, dim3(tiles(g.M, g.N)), dim3(256), 0, st, g);
-    }
-    int rc = launch_status("pb_lmhead_ce_bwd(dlogits)");
+    int rc = dlogits_chunk(x, ldx, w, ldw, n, v, d, targets, ignore_index, z_loss_coeff, lse,
+                           grad_out, v0, vc, dl, ldl, dlt, ldlt, round_bf16, logits, ldlg, st);
     if (rc) return rc;
     // 2) dx (+)= dL W_chunk: A = dL [n][vc], B = W^T[:, v0:v0+vc] rows d.
     GemmArgs gx = {};
@@ -1208,4 +1219,37 @@ extern "C" int pb_lmhead_ce_bwd_logits(const void *x, int64_t ldx, const void *w
   return lmhead_bwd(x, ldx, w, ldw, xt, ldxt, wt, ldwt, n, v, d, targets, ignore_index,
                     z_loss_coeff, lse, grad_out, vchunk, workspace, dx, dx_dtype, lddx, dw,
                     dw_dtype, lddw, dw_accumulate, logits_dtype == PB_BF16, logits, ldlg, stream);
+}
+
+extern "C" int pb_lmhead_ce_dlogits(const void *x, int64_t ldx, const void *w, int64_t ldw,
+                                    int64_t n, int64_t v, int64_t d, const int64_t *targets,
+                                    int64_t ignore_index, float z_loss_coeff, const float *lse,
+                                    const float *grad_out, int64_t v0, int64_t vc, void *dl,
+                                    int64_t ldl, void *dlt, int64_t ldlt, int logits_dtype,
+                                    const void *logits, int64_t ldlg, void *stream) {
+  using namespace pb;
+  using namespace pb::ce;
+  clear_error();
+  PB_CHECK_ARG(n >= 1 && v >= 1 && d >= 1 && vc >= 1 && v0 >= 0 && v0 + vc <= v,
+               "pb_lmhead_ce_dlogits: bad shape or chunk");
+  PB_CHECK_SUPPORTED(n < (1LL << 31) && v < (1LL << 31) && d < (1LL << 31),
+                     "pb_lmhead_ce_dlogits: too large");
+  PB_CHECK_ARG(logits_dtype == PB_BF16 || logits_dtype == PB_F32,
+               "pb_lmhead_ce_dlogits: logits_dtype must be bf16 or fp32");
+  PB_CHECK_ARG(x && w && targets && lse && grad_out && dl && dlt,
+               "pb_lmhead_ce_dlogits: null argument");
+  PB_CHECK_ARG(k_aligned(x, ldx) && k_aligned(w, ldw) && d % 8 == 0 && k_aligned(dl, ldl) &&
+                   k_aligned(dlt, ldlt) && ldl >= vc && ldlt >= n,
+               "pb_lmhead_ce_dlogits: operands must be 16-byte aligned with row strides %% 8 == 0 "
+               "(ldl >= vc, ldlt >= n)");
+  PB_CHECK_ARG(logits == nullptr || (ldlg >= n && ldlg % 8 == 0 &&
+                                     reinterpret_cast<uintptr_t>(logits) % 16 == 0),
+               "pb_lmhead_ce_dlogits: logits must be 16-byte aligned with ldlg >= n, "
+               "ldlg %% 8 == 0");
+  PB_CHECK_SUPPORTED(logits == nullptr || (n + kDlTokens - 1) / kDlTokens <= 65535,
+                     "pb_lmhead_ce_dlogits: too many rows for stored logits");
+  return dlogits_chunk(x, ldx, w, ldw, n, v, d, targets, ignore_index, z_loss_coeff, lse,
+                       grad_out, v0, (int)vc, static_cast<bf16_t *>(dl), ldl,
+                       static_cast<bf16_t *>(dlt), ldlt, logits_dtype == PB_BF16, logits, ldlg,
+                       as_stream(stream));
 }

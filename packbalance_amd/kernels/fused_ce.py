@@ -22,8 +22,12 @@ streams the vocabulary in chunks (``vocab_chunk``: as many vocab rows as keep
 one dlogits chunk of all tokens under ``CHUNK_BUDGET`` elements -- 1 GiB of
 bf16 per layout -- but at least 8192): the chunk's dlogits (bf16) come from
 one memory-bound pass over the stored logits, or from a GEMM that recomputes
-them, then two GEMMs accumulate dx and write the chunk's dW rows.  Fewer, longer chunks mean fewer passes over the
-fp32 dx accumulator (cfg4: 4 chunks of 32768 rows instead of 16 of 8192).
+them (the kernel of ``pb_lmhead_ce_dlogits``), then two plain library GEMMs
+(torch on hipBLASLt) accumulate dx and write the chunk's dW rows; the C
+boundary's ``pb_lmhead_ce_bwd`` runs the same steps with this build's own
+GEMMs for C callers, and so does ``linear_cross_entropy_accumulate`` (the
+training step's form, run on two streams at once inside a captured graph).  Fewer, longer chunks mean fewer passes over the fp32 dx
+accumulator (cfg4: 4 chunks of 32768 rows instead of 16 of 8192).
 Operands are bf16 with fp32 accumulation (as the reference's autocast GEMM
 rounds them), except for fp32 x and W outside bf16 autocast: there the
 reference's logits are an fp32 product, and so are these (``_LinearCEF32``:
@@ -156,15 +160,57 @@ def _ce_forward(xb, wb, t, n, v, d8, ignore_index, z, rows, lse, total, dev, str
     return lg
 
 
-def _ce_backward(xb, wb, xt, wt, t, lse, go, lg, lg_dtype, n, v, d8, ignore_index, z, vchunk,
-                 ws, dx, dw, dw_dtype_code, dw_accumulate, stream):
-    """Backward launch: from the stored logits ``lg`` when given, else recomputing them."""
+def _ce_backward_kernels(xb, wb, xt, wt, t, lse, go, lg, lg_dtype, n, v, d8, ignore_index, z,
+                         vchunk, dx, dw, dw_accumulate):
+    """Backward on this build's own kernels (``pb_lmhead_ce_bwd_logits``: dlogits and the
+    dx / dW DMA GEMMs, which read the transposed ``xt`` and ``wt``): the training step's
+    path, whose two micro-batch streams run it concurrently inside one captured graph."""
+    ws = torch.empty(N.lib().pb_lmhead_ce_bwd_workspace_bytes(n, v, d8, vchunk),
+                     dtype=torch.uint8, device=xb.device)
     N.call("pb_lmhead_ce_bwd_logits", xb.data_ptr(), xb.stride(0), wb.data_ptr(), wb.stride(0),
            xt.data_ptr(), xt.stride(0), wt.data_ptr(), wt.stride(0), n, v, d8, t.data_ptr(),
            ignore_index, z, lse.data_ptr(), go.data_ptr(), vchunk, ws.data_ptr(), dx.data_ptr(),
-           N.dtype_code(dx), dx.stride(0), dw.data_ptr(), dw_dtype_code, dw.stride(0),
-           dw_accumulate, _lg_code(lg_dtype), N.ptr(lg), lg.stride(0) if lg is not None else 0,
-           stream)
+           N.dtype_code(dx), dx.stride(0), dw.data_ptr(),
+           N.PB_F32 if dw_accumulate else N.dtype_code(dw), dw.stride(0), int(dw_accumulate),
+           _lg_code(lg_dtype), N.ptr(lg), lg.stride(0) if lg is not None else 0,
+           N.stream_ptr(xb))
+
+
+def _ce_backward(xb, wb, t, lse, go, lg, lg_dtype, n, v, d8, ignore_index, z, vchunk, dx, dw,
+                 dw_accumulate):
+    """Backward, vocab chunk by vocab chunk: the chunk's dL [n, vc] and dL^T [vc, n]
+    (bf16) from ``pb_lmhead_ce_dlogits`` -- from the stored logits ``lg`` when given,
+    else recomputing them --, then dx (+)= dL W_chunk into an fp32 accumulator and
+    dW_chunk (+)= dL^T x as library GEMMs (torch -> hipBLASLt, fp32 accumulation),
+    which run these plain products faster than this build's own DMA GEMM
+    (``pb_lmhead_ce_bwd``; at a cfg4 chunk dx 977 vs 1,110 us and dW 809 vs 967 us)
+    and read x and W as they are, with no transposed copies."""
+    dev = xb.device
+    stream = N.stream_ptr(xb)
+    dl = torch.empty((n, vchunk), dtype=torch.bfloat16, device=dev)
+    dlt = torch.empty((vchunk, _round8(n)), dtype=torch.bfloat16, device=dev)
+    acc = dx if dx.dtype == torch.float32 else torch.empty((n, d8), dtype=torch.float32,
+                                                           device=dev)
+    for c, v0 in enumerate(range(0, v, vchunk)):
+        vc = min(vchunk, v - v0)
+        N.call("pb_lmhead_ce_dlogits", xb.data_ptr(), xb.stride(0), wb.data_ptr(), wb.stride(0),
+               n, v, d8, t.data_ptr(), ignore_index, z, lse.data_ptr(), go.data_ptr(), v0, vc,
+               dl.data_ptr(), dl.stride(0), dlt.data_ptr(), dlt.stride(0), _lg_code(lg_dtype),
+               N.ptr(lg), lg.stride(0) if lg is not None else 0, stream)
+        dlc, dltc, dwc = dl[:, :vc], dlt[:vc, :n], dw[v0:v0 + vc]
+        # beta 0 on the first chunk: the accumulator's old contents are not read
+        torch.addmm(acc, dlc, wb[v0:v0 + vc], beta=0 if c == 0 else 1,
+                    out_dtype=torch.float32, out=acc)
+        if dw_accumulate or dwc.dtype == torch.float32:
+            torch.addmm(dwc, dltc, xb, beta=1 if dw_accumulate else 0, out_dtype=torch.float32,
+                        out=dwc)
+        elif dwc.dtype == torch.bfloat16:
+            torch.mm(dltc, xb, out=dwc)
+        else:  # fp16 weights: the product in fp32, rounded once
+            dwc.copy_(torch.addmm(torch.empty((vc, d8), dtype=torch.float32, device=dev), dltc, xb,
+                                  beta=0, out_dtype=torch.float32))
+    if acc is not dx:
+        dx.copy_(acc)
 
 
 def vocab_chunk(n: int, v: int) -> int:
@@ -262,16 +308,12 @@ class _FusedLinearCE(torch.autograd.Function):
         n, d8 = xb.shape
         v = wb.shape[0]
         dev = xb.device
-        xt = _transpose_bf16(xb)  # [d8, n8]
-        wt = _transpose_bf16(wb)  # [d8, v8]
         vchunk = vocab_chunk(n, v)
-        ws = torch.empty(N.lib().pb_lmhead_ce_bwd_workspace_bytes(n, v, d8, vchunk),
-                         dtype=torch.uint8, device=dev)
         dx = torch.empty((n, d8), dtype=ctx.x_dtype, device=dev)
         dw = torch.empty((v, d8), dtype=ctx.w_dtype, device=dev)
         go = grad_output.detach().to(torch.float32).reshape(1).contiguous()
-        _ce_backward(xb, wb, xt, wt, t, lse, go, lg, ctx.lg_dtype, n, v, d8, ctx.ignore_index,
-                     ctx.z, vchunk, ws, dx, dw, N.dtype_code(dw), 0, N.stream_ptr(xb))
+        _ce_backward(xb, wb, t, lse, go, lg, ctx.lg_dtype, n, v, d8, ctx.ignore_index, ctx.z,
+                     vchunk, dx, dw, False)
         d = ctx.d
         if d8 != d:
             dx, dw = dx[:, :d], dw[:, :d]
@@ -328,7 +370,11 @@ def _fp32_operands(x: torch.Tensor, weight: torch.Tensor) -> bool:
 
 class _LMHeadCEAccum(torch.autograd.Function):
     """``_FusedLinearCE`` over a caller-held bf16 weight ``wb`` [V, d8] and its transpose
-    ``wt`` [d8, >= V], adding dW (fp32) into ``dw_acc`` instead of returning it."""
+    ``wt`` [d8, >= V], adding dW (fp32) into ``dw_acc`` instead of returning it.  The
+    backward runs on this build's own kernels (``_ce_backward_kernels``), not the library
+    GEMMs of ``linear_cross_entropy``: the training step runs it on two streams at once
+    inside one captured graph, and with the library's long-K products there the step did
+    not complete."""
 
     @staticmethod
     def forward(ctx, x, wb, wt, dw_acc, targets, ignore_index, z_loss_coeff, weight_dtype):
@@ -364,12 +410,10 @@ class _LMHeadCEAccum(torch.autograd.Function):
             raise ValueError("lmhead CE: dW accumulator width must equal the padded feature count")
         xt = _transpose_bf16(xb)
         vchunk = vocab_chunk(n, v)
-        ws = torch.empty(N.lib().pb_lmhead_ce_bwd_workspace_bytes(n, v, d8, vchunk),
-                         dtype=torch.uint8, device=dev)
         dx = torch.empty((n, d8), dtype=ctx.x_dtype, device=dev)
         go = grad_output.detach().to(torch.float32).reshape(1).contiguous()
-        _ce_backward(xb, wb, xt, wt, t, lse, go, lg, ctx.lg_dtype, n, v, d8, ctx.ignore_index,
-                     ctx.z, vchunk, ws, dx, dw, N.PB_F32, 1, N.stream_ptr(xb))
+        _ce_backward_kernels(xb, wb, xt, wt, t, lse, go, lg, ctx.lg_dtype, n, v, d8,
+                             ctx.ignore_index, ctx.z, vchunk, dx, dw, True)
         if d8 != ctx.d:
             dx = dx[:, :ctx.d]
         return dx.reshape(ctx.x_shape), None, None, None, None, None, None, None

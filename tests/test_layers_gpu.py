@@ -146,9 +146,12 @@ def test_lmhead_ce_accumulate_matches_linear_ce(dev) -> None:
     xa = x.clone().requires_grad_(True)
     loss_a = linear_cross_entropy_accumulate(xa, wb, wt, acc, t, weight_dtype=w.dtype)
     (loss_a * 1.0).backward()
+    # Same forward and dlogits; the dx / dW products run on the library GEMMs in
+    # linear_cross_entropy and on this build's own GEMMs in the accumulate form, so
+    # they agree to fp32 summation order (dx is bf16: within one rounding step).
     assert torch.equal(loss_a, loss)
-    assert torch.equal(xa.grad, xr.grad)
-    torch.testing.assert_close(acc - acc0, wr.grad, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(xa.grad.float(), xr.grad.float(), rtol=1e-2, atol=1e-4)
+    torch.testing.assert_close(acc - acc0, wr.grad, rtol=1e-4, atol=1e-5)
     with pytest.raises(ValueError):
         linear_cross_entropy_accumulate(xa, wb, wt, acc.to(BF), t)
     # bf16 W: both with bf16 logits (the default weight_dtype is wb's)
@@ -161,5 +164,5 @@ def test_lmhead_ce_accumulate_matches_linear_ce(dev) -> None:
     loss_a2 = linear_cross_entropy_accumulate(xa2, wb, wt, acc2, t)
     loss_a2.backward()
     assert torch.equal(loss_a2, loss2)
-    assert torch.equal(xa2.grad, xr2.grad)
+    torch.testing.assert_close(xa2.grad.float(), xr2.grad.float(), rtol=1e-2, atol=1e-4)
     torch.testing.assert_close(acc2 - acc0, wr2.grad.float(), rtol=1e-2, atol=1e-5)
