@@ -73,6 +73,18 @@ def test_vocab_chunk_budget() -> None:
         assert n * c <= max(CHUNK_BUDGET, n * VOCAB_CHUNK)
 
 
+def test_ce_dlogits_rejects_bad_chunks_on_host() -> None:
+    """pb_lmhead_ce_dlogits validates the vocab chunk and the strides before any launch."""
+    lib = N.lib()
+    args = lambda v0, vc, ldl, lg_dtype: (  # noqa: E731
+        16, 8, 16, 8, 8, 64, 8, 16, -100, 0.0, 16, 16, v0, vc, 16, ldl, 16, 8, lg_dtype, None, 0,
+        None)
+    assert lib.pb_lmhead_ce_dlogits(*args(60, 8, 8, N.PB_BF16)) == N.PB_EINVAL  # past v
+    assert b"chunk" in lib.pb_last_error()
+    assert lib.pb_lmhead_ce_dlogits(*args(0, 16, 8, N.PB_BF16)) == N.PB_EINVAL  # ldl < vc
+    assert lib.pb_lmhead_ce_dlogits(*args(0, 8, 8, 99)) == N.PB_EINVAL  # logits dtype
+
+
 def test_ce_backward_split_k_choice_on_host() -> None:
     """The dx product's split-K count, read back from the backward workspace size
     (dL, dL^T, the fp32 dx accumulator, then one fp32 [n, d] partial per split):
