@@ -377,6 +377,62 @@ def attention_kernels(dev, iters: int) -> dict:
     }
 
 
+PEAK_FP32_TFLOPS = 157.3  # MI355X dense fp32
+
+
+def attention_f32_kernels(dev, iters: int) -> dict:
+    """The fp32 attention path (fp32 q/k/v without autocast, where the reference's
+    FlexAttention computes in fp32) at the cfg2 attention shape: the first step's
+    first [2, 2048] micro-batch, Hq 12, Hkv 4, D 64.  Labelled, not a headline: these
+    kernels are the precision path (one wave per row on the VALU, no MFMA)."""
+    import torch
+
+    from packbalance_amd import _native as N
+    from packbalance_amd.data import workloads as W
+
+    packs = W.cfg2_steps(1)[0][:2]
+    B, S, Hq, Hkv, D = 2, 2048, 12, 4, 64
+    doc = W.doc_ids_from_lengths(packs, S).to(dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = torch.randn(B, S, Hq, D, device=dev, generator=g).transpose(1, 2)
+    k = torch.randn(B, S, Hkv, D, device=dev, generator=g).transpose(1, 2)
+    v = torch.randn(B, S, Hkv, D, device=dev, generator=g).transpose(1, 2)
+    do = torch.randn(B, S, Hq, D, device=dev, generator=g).transpose(1, 2)
+    out = torch.empty(B, S, Hq, D, device=dev).transpose(1, 2)
+    dq = torch.empty_like(out)
+    dk = torch.empty(B, S, Hkv, D, device=dev).transpose(1, 2)
+    dv = torch.empty_like(dk)
+    lse = torch.empty(B, Hq, S, device=dev)
+    delta = torch.empty(B, Hq, S, device=dev)
+    sc, st = 1.0 / D ** 0.5, N.stream_ptr(q)
+
+    def fwd():
+        N.call("pb_attn_fwd_f32", N.BHSD.of(q), N.BHSD.of(k), N.BHSD.of(v), N.BHSD.of(out),
+               lse.data_ptr(), doc.data_ptr(), doc.stride(0), B, Hq, Hkv, S, D, sc, st)
+
+    def bwd():
+        N.call("pb_attn_bwd_f32", N.BHSD.of(q), N.BHSD.of(k), N.BHSD.of(v), N.BHSD.of(out),
+               N.BHSD.of(do), N.BHSD.of(dq), N.BHSD.of(dk), N.BHSD.of(dv), lse.data_ptr(),
+               delta.data_ptr(), doc.data_ptr(), doc.stride(0), B, Hq, Hkv, S, D, sc, st)
+
+    fwd()
+    bwd()
+    torch.cuda.synchronize()
+    t_f = events_ms(fwd, iters)
+    t_b = events_ms(bwd, iters)
+    pairs = float(W.attention_pairs(packs))
+    f_fwd, f_bwd = 4.0 * D * Hq * pairs, 8.0 * D * Hq * pairs
+    return {
+        "workload": "cfg2 attention shape in fp32: [2, 2048] micro-batch, Hq 12, Hkv 4, D 64",
+        "allowed_pairs_per_head": pairs,
+        "fwd_ms": t_f, "bwd_ms": t_b,
+        "fwd_bwd_tflops": (f_fwd + f_bwd) / (t_f + t_b) / 1e9,
+        "frac_fp32_peak": (f_fwd + f_bwd) / (t_f + t_b) / 1e9 / PEAK_FP32_TFLOPS,
+        "note": "precision path (pb_attn_fwd_f32 / pb_attn_bwd_f32): one wave per row on the "
+                "VALU, no MFMA; fraction of the 157.3 TFLOP/s dense fp32 peak",
+    }
+
+
 def lmhead_ce_kernels(dev, iters: int, vchunk: int = 8192, stored: bool = False) -> dict:
     import torch
 
@@ -580,7 +636,8 @@ def main() -> int:
                     help="packs run as one [k, 2048] micro-batch (1, 2 or 4)")
     ap.add_argument("--streams", type=int, default=2,
                     help="streams the step's micro-batches run on concurrently (1: one after another)")
-    ap.add_argument("--only", choices=["train", "attention", "lmhead_ce", "lmhead_ce_stored",
+    ap.add_argument("--only", choices=["train", "attention", "attention_f32", "lmhead_ce",
+                                       "lmhead_ce_stored",
                                        "ce_rows", "norm_act", "copy", "peaks"],
                     default=None, help="run one part only (for profiling)")
     args = ap.parse_args()
@@ -604,6 +661,7 @@ def main() -> int:
     if args.only and args.only != "train":
         flush = make_flush(dev)
         fn = {"attention": lambda: attention_kernels(dev, args.kernel_iters),
+              "attention_f32": lambda: attention_f32_kernels(dev, args.kernel_iters),
               "lmhead_ce": lambda: lmhead_ce_kernels(dev, args.kernel_iters),
               "lmhead_ce_stored": lambda: lmhead_ce_kernels(dev, args.kernel_iters, stored=True),
               "ce_rows": lambda: ce_rows_kernel(dev, args.kernel_iters, flush),
@@ -630,6 +688,8 @@ def main() -> int:
         flush = make_flush(dev)
         log("kernels: attention (cfg3)")
         kernels["attention"] = attention_kernels(dev, args.kernel_iters)
+        log("kernels: attention, fp32 path (cfg2 shape, labelled)")
+        kernels["attention_f32"] = attention_f32_kernels(dev, max(2, args.kernel_iters // 2))
         a = kernels["attention"]
         roofline = {"bound": "mfma",
                     "kernel": "document-masked attention fwd+bwd at cfg3: pb_attn_fwd + pb_attn_bwd "
