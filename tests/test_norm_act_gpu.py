@@ -109,6 +109,66 @@ def test_rmsnorm_cfg5_full_size(dev) -> None:
     _close(wr.grad, dw_ref, 1e-2, "dw")
 
 
+def _bwd_abi(dy, x, w, rstd, ws):
+    rows, n = x.shape
+    dx, dw = torch.empty_like(x), torch.empty_like(w)
+    N.call("pb_rmsnorm_bwd", dy.data_ptr(), dy.stride(0), x.data_ptr(), x.stride(0),
+           N.dtype_code(x), w.data_ptr(), N.dtype_code(w), rstd.data_ptr(), dx.data_ptr(),
+           dx.stride(0), dw.data_ptr(), ws.data_ptr(), rows, n, N.stream_ptr(x))
+    return dx, dw
+
+
+@pytest.mark.parametrize("rows,n,dtype", [
+    (32768, 4096, torch.bfloat16),  # 512 workgroups: 512 dW partial rows
+    (40, 768, torch.float32),       # 5 workgroups
+    (8, 4096, torch.bfloat16),      # one workgroup, one partial row
+    (3000, 99, torch.float32),      # n % 4 != 0: the streaming kernel
+])
+def test_rmsnorm_bwd_workspace_reuse(rows, n, dtype, dev) -> None:
+    """One workspace serves call after call (sizes changing, stale partial rows of a
+    larger call left in it): results repeat bit for bit and dw matches the oracle."""
+    x, w, dy = _rms_case((rows, n), dtype, dtype, dev, seed=3)
+    rstd = torch.rsqrt(x.float().pow(2).mean(-1) + 1e-5).contiguous()
+    ws = torch.empty(N.lib().pb_rmsnorm_bwd_workspace_bytes(32768, 4096) + 4096,
+                     dtype=torch.uint8, device=dev)
+    assert N.lib().pb_rmsnorm_bwd_workspace_bytes(rows, n) <= ws.numel()
+    ws.fill_(0x7f)  # stale contents: every partial row must be written before it is read
+    first = _bwd_abi(dy, x, w, rstd, ws)
+    for _ in range(2):
+        dx, dw = _bwd_abi(dy, x, w, rstd, ws)
+        torch.cuda.synchronize()
+        assert torch.equal(dx, first[0]) and torch.equal(dw, first[1])
+    _, dw_ref = OK.rmsnorm_bwd(dy, x, w, 1e-5)
+    _close(first[1], dw_ref, max(TOL[dtype], 1e-4), "dw")
+
+
+def test_rmsnorm_bwd_graph_replays(dev) -> None:
+    """The backward (fused dx + dW partials, then the dW reduce) captured in a HIP graph:
+    every replay, with eager work between them, equals the eager result."""
+    x, w, dy = _rms_case((4096, 4096), torch.bfloat16, torch.bfloat16, dev, seed=4)
+    xr = x.clone().requires_grad_(True)
+    wr = w.clone().requires_grad_(True)
+    rmsnorm(xr, wr, 1e-5).backward(dy)  # eager
+    want_dx, want_dw = xr.grad.clone(), wr.grad.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            xr.grad = wr.grad = None
+            rmsnorm(xr, wr, 1e-5).backward(dy)
+    torch.cuda.current_stream().wait_stream(s)
+    xr.grad = wr.grad = None
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        y = rmsnorm(xr, wr, 1e-5)
+        y.backward(dy)
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(xr.grad, want_dx) and torch.equal(wr.grad, want_dw)
+        rmsnorm(xr.detach(), w, 1e-5).sum().item()  # eager work between replays
+
+
 def test_rmsnorm_rejects_cpu_and_huge() -> None:
     with pytest.raises(RuntimeError):
         rmsnorm(torch.randn(2, 8), torch.ones(8), 1e-5)
