@@ -307,15 +307,15 @@ def cpu_kernel_baselines() -> dict:
 
 
 # ---------------------------------------------------------------- kernels
-def attention_kernels(dev, iters: int) -> dict:
+def _attention_timing(dev, iters: int, packs, B: int, S: int, Hq: int, Hkv: int, D: int):
+    """Event-timed pb_attn_fwd / pb_attn_bwd (bf16, plans built beforehand) on `packs`:
+    (fwd_ms, bwd_ms, fwd FLOPs, bwd FLOPs, allowed pairs per head, doc ids)."""
     import torch
 
     from packbalance_amd import _native as N
     from packbalance_amd.data import workloads as W
     from packbalance_amd.model import attention as A
 
-    packs = W.cfg3_packs()
-    B, S, Hq, Hkv, D = 8, 8192, 32, 8, 128
     doc = W.doc_ids_from_lengths(packs, S).to(dev)
     torch.manual_seed(0)
     q = torch.randn(B, S, Hq, D, device=dev, dtype=torch.bfloat16).transpose(1, 2)
@@ -352,8 +352,16 @@ def attention_kernels(dev, iters: int) -> dict:
     t_f = events_ms(fwd, iters)
     t_b = events_ms(bwd, iters)
     pairs = float(W.attention_pairs(packs))
-    f_fwd = 4.0 * D * Hq * pairs
-    f_bwd = 8.0 * D * Hq * pairs
+    return t_f, t_b, 4.0 * D * Hq * pairs, 8.0 * D * Hq * pairs, pairs, doc
+
+
+def attention_kernels(dev, iters: int) -> dict:
+    from packbalance_amd.data import workloads as W
+    from packbalance_amd.model import attention as A
+
+    packs = W.cfg3_packs()
+    B, S, Hq, Hkv, D = 8, 8192, 32, 8, 128
+    t_f, t_b, f_fwd, f_bwd, pairs, doc = _attention_timing(dev, iters, packs, B, S, Hq, Hkv, D)
     # Secondary, tile-size dependent: every 128 x 128 block with at least one
     # allowed pair (FlexAttention's PARTIAL + FULL blocks) counted as dense.
     blocks = 0
@@ -377,6 +385,24 @@ def attention_kernels(dev, iters: int) -> dict:
     }
 
 
+def attention_cfg2_kernels(dev, iters: int) -> dict:
+    """The attention of one cfg2 micro-batch (the first step's first two packs as one
+    [2, 2048] batch, Hq 12, Hkv 4, D 64, bf16), as each layer of the training step runs
+    it.  Labelled, not the roofline: a small, launch- and VALU-bound problem."""
+    from packbalance_amd.data import workloads as W
+
+    packs = W.cfg2_steps(1)[0][:2]
+    B, S, Hq, Hkv, D = 2, 2048, 12, 4, 64
+    t_f, t_b, f_fwd, f_bwd, pairs, _ = _attention_timing(dev, iters, packs, B, S, Hq, Hkv, D)
+    return {
+        "workload": "cfg2 micro-batch: [2, 2048] (step 1, packs 0-1), Hq 12, Hkv 4, D 64, bf16",
+        "allowed_pairs_per_head": pairs,
+        "fwd_us": t_f * 1e3, "bwd_us": t_b * 1e3,
+        "fwd_bwd_tflops": (f_fwd + f_bwd) / (t_f + t_b) / 1e9,
+        "frac_bf16_peak": (f_fwd + f_bwd) / (t_f + t_b) / 1e9 / PEAK_BF16_TFLOPS,
+    }
+
+
 PEAK_FP32_TFLOPS = 157.3  # MI355X dense fp32
 
 
@@ -384,7 +410,7 @@ def attention_f32_kernels(dev, iters: int) -> dict:
     """The fp32 attention path (fp32 q/k/v without autocast, where the reference's
     FlexAttention computes in fp32) at the cfg2 attention shape: the first step's
     first [2, 2048] micro-batch, Hq 12, Hkv 4, D 64.  Labelled, not a headline: these
-    kernels are the precision path (one wave per row on the VALU, no MFMA)."""
+    kernels are the precision path (fp32 operands on v_mfma_f32_32x32x2_f32)."""
     import torch
 
     from packbalance_amd import _native as N
@@ -428,8 +454,9 @@ def attention_f32_kernels(dev, iters: int) -> dict:
         "fwd_ms": t_f, "bwd_ms": t_b,
         "fwd_bwd_tflops": (f_fwd + f_bwd) / (t_f + t_b) / 1e9,
         "frac_fp32_peak": (f_fwd + f_bwd) / (t_f + t_b) / 1e9 / PEAK_FP32_TFLOPS,
-        "note": "precision path (pb_attn_fwd_f32 / pb_attn_bwd_f32): one wave per row on the "
-                "VALU, no MFMA; fraction of the 157.3 TFLOP/s dense fp32 peak",
+        "note": "precision path (pb_attn_fwd_f32 / pb_attn_bwd_f32): fp32 MFMA, one workgroup "
+                "per 128-row tile walks its whole KV (or query) list, so the longest document "
+                "sets the time; fraction of the 157.3 TFLOP/s dense fp32 peak",
     }
 
 
@@ -636,7 +663,8 @@ def main() -> int:
                     help="packs run as one [k, 2048] micro-batch (1, 2 or 4)")
     ap.add_argument("--streams", type=int, default=2,
                     help="streams the step's micro-batches run on concurrently (1: one after another)")
-    ap.add_argument("--only", choices=["train", "attention", "attention_f32", "lmhead_ce",
+    ap.add_argument("--only", choices=["train", "attention", "attention_cfg2", "attention_f32",
+                                       "lmhead_ce",
                                        "lmhead_ce_stored",
                                        "ce_rows", "norm_act", "copy", "peaks"],
                     default=None, help="run one part only (for profiling)")
@@ -661,6 +689,7 @@ def main() -> int:
     if args.only and args.only != "train":
         flush = make_flush(dev)
         fn = {"attention": lambda: attention_kernels(dev, args.kernel_iters),
+              "attention_cfg2": lambda: attention_cfg2_kernels(dev, max(20, args.kernel_iters)),
               "attention_f32": lambda: attention_f32_kernels(dev, args.kernel_iters),
               "lmhead_ce": lambda: lmhead_ce_kernels(dev, args.kernel_iters),
               "lmhead_ce_stored": lambda: lmhead_ce_kernels(dev, args.kernel_iters, stored=True),
@@ -688,6 +717,8 @@ def main() -> int:
         flush = make_flush(dev)
         log("kernels: attention (cfg3)")
         kernels["attention"] = attention_kernels(dev, args.kernel_iters)
+        log("kernels: attention at the cfg2 micro-batch shape (labelled)")
+        kernels["attention_cfg2"] = attention_cfg2_kernels(dev, max(20, args.kernel_iters))
         log("kernels: attention, fp32 path (cfg2 shape, labelled)")
         kernels["attention_f32"] = attention_f32_kernels(dev, max(2, args.kernel_iters // 2))
         a = kernels["attention"]

@@ -1,21 +1,36 @@
-// Document-masked causal GQA attention in fp32 (gfx950, wave64, no MFMA).
+// Document-masked causal GQA attention in fp32 on the fp32 matrix cores
+// (gfx950 v_mfma_f32_32x32x2_f32: fp32 operands, fp32 accumulation).
 //
 // The path for fp32 q/k/v: without autocast the reference's FlexAttention
 // computes in fp32 (packbalance/model/attention.py:116-122 on fp32 tensors),
-// while the MFMA kernels (attn_fwd.hip / attn_bwd.hip) take bf16 operands.
+// while the bf16 kernels (attn_fwd.hip / attn_bwd.hip) round operands to bf16.
 // Same mask and conventions as those kernels: allowed(i, j) = doc[i] == doc[j]
 // && j <= i (padding -1 is one more document, as FlexAttention's mask_mod),
 // query head h reads KV head h / (Hq / Hkv), lse in the log2 domain
 // (log2 sum_j exp2(scale log2(e) q.k)).
 //
-// One wave per row, no tiles and no barriers: the forward and dQ kernels walk
-// one query row's keys, the dK/dV kernel one key row's queries (over its GQA
-// group), 64 rows of the other axis per step with lane <-> row for the dot
-// products (each lane reads its row, float4 when D % 4 == 0) and lane <-> head
-// dim (d = lane, lane + 64) for the row-weighted sums, the weights broadcast by
-// readlane.  A step whose 64 rows hold no allowed pair is skipped (one document
-// load per lane decides it), so the work follows the documents.  This is the
-// precision path (cfg1-sized problems), not a throughput kernel.
+// Tiles as in the bf16 kernels, with fp32 operands read one float per lane
+// and MFMA (k = 2 per instruction):
+//   forward / dQ  one workgroup per (pack, query head, 128 query rows), wave w
+//                 owning 32 query rows with its Q (and dO) row in registers;
+//                 S^T = K Q^T per 32-row KV sub-tile (lane <-> query column),
+//                 then O^T += V^T P^T (forward) or dQ^T += K^T dS^T (dQ), with
+//                 P^T / dS^T taken straight from the accumulators as the B
+//                 operand (register r of lane half h is KV row crow(h, r), the
+//                 same row the A operand of that lane reads).  The dQ kernel
+//                 also forms delta = rowsum(dO * O) for the dK/dV kernel.
+//   dK / dV       one workgroup per (pack, KV head, 128 KV rows), wave w owning
+//                 32 KV rows with K and V in registers; it walks every query
+//                 head of the GQA group and every 32-row query sub-tile at or
+//                 after its rows: S = Q K^T and dP = dO V^T (lane <-> KV
+//                 column), then dV^T += dO^T P and dK^T += Q^T dS.
+// K / V (or Q / dO) sub-tiles pass through LDS (row pitch DP + 1 floats),
+// staged in registers one sub-tile ahead; the head dim is padded to DP (32,
+// 64 or 128) with zeros.  A workgroup first lists the sub-tiles that hold an
+// allowed pair for any of its rows (its rows' document runs against every
+// position of the other axis, visit_list) and loads only those; a wave then
+// skips a listed sub-tile whose 32 x 32 pairs hold none for its own rows.  So
+// the work follows the documents, and nothing past the causal bound is read.
 #include "attn_common.hpp"
 
 namespace pb {
@@ -37,197 +52,486 @@ struct Args {
   int64_t doc_sb;
   int B, Hq, Hkv, S, D;
   float scale;  // softmax scale
-  int vec;      // rows may be read as float4 (D % 4 == 0, 16-byte aligned rows)
+  int vec;      // K / V / Q / dO rows may be read as float4 (D % 4 == 0, 16-byte aligned rows)
 };
 
-constexpr int kWaves = 4;  // one row per wave, four per workgroup
+using attn::f32x16_t;
+using attn::zero16;
 
-// dot(x, row) over the head dim, x in LDS (broadcast reads), row in global.
-__device__ __forceinline__ float dot_row(const float *x, const float *row, int D, int vec) {
-  float s = 0.f;
-  if (vec) {
-    for (int d = 0; d < D; d += 4) {
-      const float4 r = *reinterpret_cast<const float4 *>(row + d);
-      s = fmaf(x[d], r.x, s);
-      s = fmaf(x[d + 1], r.y, s);
-      s = fmaf(x[d + 2], r.z, s);
-      s = fmaf(x[d + 3], r.w, s);
+constexpr int kWaves = 4;           // waves per workgroup
+constexpr int kRows = 32 * kWaves;  // rows per workgroup (query rows, or KV rows for dK/dV)
+
+__device__ __forceinline__ f32x16_t mfma(float a, float b, const f32x16_t &c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// Row of a 32 x 32 MFMA accumulator held in register r by lane half h.
+__device__ __forceinline__ int crow(int h, int r) { return 8 * (r >> 2) + 4 * h + (r & 3); }
+
+__device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32); }
+
+// A [32][DP] fp32 sub-tile (rows r0 .. r0 + 31 of one (pack, head) view,
+// columns past D and rows past S zero), staged in registers by the
+// workgroup's 256 threads and stored to LDS at pitch DP + 1.
+template <int DP>
+struct Tile {
+  static constexpr int N = 32 * DP / (64 * kWaves);  // floats per thread
+  float v[N];
+  __device__ __forceinline__ void load(const View &t, int b, int hh, int r0, int S, int D,
+                                       bool vec) {
+    const int tid = threadIdx.x;
+    if (vec) {  // 16-byte chunks (D % 4 == 0)
+#pragma unroll
+      for (int i = 0; i < N / 4; ++i) {
+        const int e = tid + 64 * kWaves * i;
+        const int row = e / (DP / 4), col = (e % (DP / 4)) * 4;
+        float4 x = {0.f, 0.f, 0.f, 0.f};
+        if (r0 + row < S && col < D) x = *reinterpret_cast<const float4 *>(t.row(b, hh, r0 + row) + col);
+        v[4 * i] = x.x;
+        v[4 * i + 1] = x.y;
+        v[4 * i + 2] = x.z;
+        v[4 * i + 3] = x.w;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        const int e = tid + 64 * kWaves * i;
+        const int row = e / DP, col = e % DP;
+        v[i] = (r0 + row < S && col < D) ? t.row(b, hh, r0 + row)[col] : 0.f;
+      }
     }
-  } else {
-    for (int d = 0; d < D; ++d) s = fmaf(x[d], row[d], s);
   }
-  return s;
-}
-
-__device__ __forceinline__ float bcast(float v, int lane) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
-}
-
-// (b, h, row) of flat row id r over [B][H][S].
-__device__ __forceinline__ void split_row(int64_t r, int H, int S, int &b, int &h, int &i) {
-  i = (int)(r % S);
-  h = (int)((r / S) % H);
-  b = (int)(r / ((int64_t)S * H));
-}
-
-__global__ __launch_bounds__(64 * kWaves) void attn_fwd_f32(Args a) {
-  __shared__ float xs[kWaves][128];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t r = (int64_t)blockIdx.x * kWaves + wave;
-  if (r >= (int64_t)a.B * a.Hq * a.S) return;  // wave-uniform; no barrier below
-  int b, h, i;
-  split_row(r, a.Hq, a.S, b, h, i);
-  const int hk = h / (a.Hq / a.Hkv);
-  const float sl2 = a.scale * kLog2e;
-  float *qx = xs[wave];
-  const float *qrow = a.q.row(b, h, i);
-  for (int d = lane; d < a.D; d += 64) qx[d] = qrow[d] * sl2;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  const int64_t *docb = a.doc + b * a.doc_sb;
-  const int64_t di = docb[i];
-  float m = -INFINITY, l = 0.f, o0 = 0.f, o1 = 0.f;
-  for (int j0 = 0; j0 <= i; j0 += 64) {
-    const int j = j0 + lane;
-    const bool ok = j <= i && docb[j <= i ? j : i] == di;
-    if (__builtin_amdgcn_ballot_w64(ok) == 0) continue;
-    const float s = ok ? dot_row(qx, a.k.row(b, hk, j), a.D, a.vec) : -INFINITY;
-    const float mc = wave_max(s);
-    const float mn = fmaxf(m, mc);
-    const float alpha = fast_exp2(m - mn);  // m = -inf on the first step: 0
-    const float p = ok ? fast_exp2(s - mn) : 0.f;
-    l = l * alpha + wave_sum(p);
-    o0 *= alpha;
-    o1 *= alpha;
-    const int n = min(64, i + 1 - j0);
-    for (int t = 0; t < n; ++t) {
-      const float pt = bcast(p, t);
-      if (pt == 0.f) continue;  // uniform: masked rows
-      const float *vr = a.v.row(b, hk, j0 + t);
-      if (lane < a.D) o0 = fmaf(pt, vr[lane], o0);
-      if (lane + 64 < a.D) o1 = fmaf(pt, vr[lane + 64], o1);
+  __device__ __forceinline__ void store(float *lds, bool vec) const {
+    const int tid = threadIdx.x;
+    if (vec) {
+#pragma unroll
+      for (int i = 0; i < N / 4; ++i) {
+        const int e = tid + 64 * kWaves * i;
+        const int row = e / (DP / 4), col = (e % (DP / 4)) * 4;
+#pragma unroll
+        for (int x = 0; x < 4; ++x) lds[row * (DP + 1) + col + x] = v[4 * i + x];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        const int e = tid + 64 * kWaves * i;
+        lds[(e / DP) * (DP + 1) + e % DP] = v[i];
+      }
     }
+  }
+};
+
+// Sub-tiles of the other axis that hold at least one allowed pair with the
+// workgroup's own rows [r0, r0 + kRows): the own rows' documents as runs, then
+// every other-axis position p in [lo, hi) against them -- q-major kernels (own
+// rows are queries, p a KV position) need doc[p] equal to a run's and p at or
+// before its last query; the KV-major kernel (own rows are KV rows, p a query)
+// needs doc[p] equal and p at or after the run's first KV row.  The 32-row
+// sub-tiles holding such a p are listed in ascending order (absolute indices);
+// returns their count, or -1 when the range has more than kMaxList sub-tiles
+// (the caller then visits every one).  Called by the whole workgroup.
+constexpr int kMaxList = 1024;
+
+struct Visit {
+  int64_t rdoc[kRows];
+  int rlo[kRows], rhi[kRows];
+  unsigned char flag[kMaxList];
+  int list[kMaxList];
+  int nrun, cnt;
+};
+
+template <bool QMAJOR>
+__device__ int visit_list(Visit &vs, const int64_t *docb, int S, int r0, int lo, int hi) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int t0 = lo / 32, nt = (hi + 31) / 32 - t0;  // lo is a multiple of 32
+  if (nt > kMaxList) return -1;                       // uniform
+  const int own_end = min(S, r0 + kRows);
+  int64_t d = 0;
+  const bool valid = tid < kRows && r0 + tid < S;
+  if (tid < kRows) {
+    d = valid ? docb[r0 + tid] : 0;
+    vs.rdoc[tid] = d;  // own documents first; the runs overwrite them below
+  }
+  for (int i = tid; i < nt; i += 64 * kWaves) vs.flag[i] = 0;
+  __syncthreads();
+  const bool start = valid && (tid == 0 || vs.rdoc[tid - 1] != d);
+  const uint64_t bal = __builtin_amdgcn_ballot_w64(start);
+  if (wave == 0 && lane == 0) vs.cnt = __popcll(bal);  // runs starting in wave 0
+  __syncthreads();
+  if (start) {
+    const int id = (wave == 1 ? vs.cnt : 0) + __popcll(bal & ((1ull << lane) - 1));
+    vs.rdoc[id] = d;
+    vs.rlo[id] = r0 + tid;
+  }
+  if (wave == 1 && lane == 0) vs.nrun = vs.cnt + __popcll(bal);
+  __syncthreads();
+  const int nrun = vs.nrun;
+  for (int j = tid; j < nrun; j += 64 * kWaves)
+    vs.rhi[j] = (j + 1 < nrun ? vs.rlo[j + 1] : own_end) - 1;
+  __syncthreads();
+  for (int p = lo + tid; p < hi; p += 64 * kWaves) {
+    const int64_t dp = docb[p];
+    bool ok = false;
+    for (int j = 0; j < nrun; ++j)
+      ok |= dp == vs.rdoc[j] && (QMAJOR ? p <= vs.rhi[j] : p >= vs.rlo[j]);
+    if (ok) vs.flag[p / 32 - t0] = 1;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    int n = 0;
+    for (int base = 0; base < nt; base += 64) {
+      const bool f = base + lane < nt && vs.flag[base + lane];
+      const uint64_t b = __builtin_amdgcn_ballot_w64(f);
+      if (f) vs.list[n + __popcll(b & ((1ull << lane) - 1))] = t0 + base + lane;
+      n += __popcll(b);
+    }
+    if (lane == 0) vs.cnt = n;
+  }
+  __syncthreads();
+  return vs.cnt;
+}
+
+// ---------------------------------------------------------------- forward
+// Head dim 128 (Q, O^T, the staged tiles and the K column reads hoisted ahead of
+// the S^T chain: ~300 registers) runs one wave per SIMD.
+template <int DP>
+__global__ __launch_bounds__(64 * kWaves)
+__attribute__((amdgpu_waves_per_eu(DP == 128 ? 1 : 2, DP == 128 ? 1 : 2)))
+void attn_fwd_f32(Args a) {
+  constexpr int P = DP + 1, NS = DP / 2, NDB = DP / 32;
+  __shared__ float Ks[32 * P], Vs[32 * P];
+  __shared__ int64_t kd[32];
+  __shared__ Visit vis;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hh = lane >> 5, l32 = lane & 31;
+  const int S = a.S, D = a.D;
+  const int nqt = (S + kRows - 1) / kRows;
+  const int qt = nqt - 1 - (int)(blockIdx.x % nqt);  // late query tiles (longest walks) first
+  const int bh = (int)(blockIdx.x / nqt), h = bh % a.Hq, b = bh / a.Hq;
+  const int hk = h / (a.Hq / a.Hkv);
+  const bool vec = a.vec != 0;
+  const int64_t *docb = a.doc + b * a.doc_sb;
+  const float sl2 = a.scale * kLog2e;
+
+  const int qi = qt * kRows + wave * 32 + l32;
+  const bool qv = qi < S;
+  const int64_t qdoc = docb[qv ? qi : S - 1];
+  float qf[NS];  // B operand of S^T = K Q^T: Q[qi][2k + hh], scaled into the log2 domain
+  {
+    const float *qr = a.q.row(b, h, qv ? qi : 0);
+#pragma unroll
+    for (int k = 0; k < NS; ++k) qf[k] = (qv && 2 * k + hh < D) ? qr[2 * k + hh] * sl2 : 0.f;
+  }
+  f32x16_t oacc[NDB];
+#pragma unroll
+  for (int i = 0; i < NDB; ++i) oacc[i] = zero16();
+  float m = -INFINITY, l = 0.f;
+
+  // KV sub-tiles up to the causal bound that hold an allowed pair for some row
+  // of the workgroup.
+  const int kv_end = min(S, (qt + 1) * kRows);
+  const int nl = visit_list<true>(vis, docb, S, qt * kRows, 0, kv_end);
+  const int nst = nl >= 0 ? nl : (kv_end + 31) / 32;
+  auto tile_of = [&](int i) { return nl >= 0 ? vis.list[i] : i; };
+  Tile<DP> tk, tv;
+  int64_t dnext = 0;
+  auto fetch = [&](int st) {
+    tk.load(a.k, b, hk, 32 * st, S, D, vec);
+    tv.load(a.v, b, hk, 32 * st, S, D, vec);
+    if (tid < 32) dnext = 32 * st + tid < S ? docb[32 * st + tid] : 0;
+  };
+  if (nst > 0) fetch(tile_of(0));
+  for (int i = 0; i < nst; ++i) {
+    __syncthreads();  // every wave is done with the previous sub-tile
+    tk.store(Ks, vec);
+    tv.store(Vs, vec);
+    if (tid < 32) kd[tid] = dnext;
+    __syncthreads();
+    const int kv0 = 32 * tile_of(i);
+    if (i + 1 < nst) fetch(tile_of(i + 1));
+    unsigned okm = 0;  // bit r: pair (KV row crow(hh, r), query qi) allowed
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kv = kv0 + crow(hh, r);
+      okm |= (unsigned)(qv && kv <= qi && kd[crow(hh, r)] == qdoc) << r;
+    }
+    if (__builtin_amdgcn_ballot_w64(okm != 0) == 0) continue;  // uniform over the wave
+    f32x16_t sacc = zero16();
+#pragma unroll
+    for (int k = 0; k < NS; ++k)
+      if (2 * k < D) sacc = mfma(Ks[l32 * P + 2 * k + hh], qf[k], sacc);
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      sacc[r] = (okm >> r) & 1 ? sacc[r] : -INFINITY;
+      mloc = fmaxf(mloc, sacc[r]);
+    }
+    mloc = fmaxf(mloc, xor32(mloc));  // the other lane half holds the other 16 KV rows
+    const float mn = fmaxf(m, mloc);
+    const float mu = mn == -INFINITY ? 0.f : mn;
+    const float alpha = fast_exp2(m - mu);  // 0 while m is -inf
     m = mn;
+    l *= alpha;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) oacc[db] *= alpha;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      sacc[r] = fast_exp2(sacc[r] - mu);
+      l += sacc[r];
+    }
+    // O^T += V^T P^T: step r pairs KV rows crow(0, r) and crow(1, r) (k = lane half).
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+      if (32 * db < D) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          oacc[db] = mfma(Vs[crow(hh, r) * P + 32 * db + l32], sacc[r], oacc[db]);
+      }
   }
-  const float inv = 1.0f / l;  // l >= 1: row i always sees itself
-  float *orow = a.o.row(b, h, i);
-  if (lane < a.D) orow[lane] = o0 * inv;
-  if (lane + 64 < a.D) orow[lane + 64] = o1 * inv;
-  if (lane == 0) a.lse[((int64_t)b * a.Hq + h) * a.S + i] = m + fast_log2(l);
+  const float lt = l + xor32(l);
+  if (!qv) return;
+  const float inv = lt > 0.f ? 1.0f / lt : 0.f;  // lt >= 1: row qi always sees itself
+  float *orow = a.o.row(b, h, qi);
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int d = 32 * db + crow(hh, r);
+      if (d < D) orow[d] = oacc[db][r] * inv;
+    }
+  if (hh == 0) a.lse[((int64_t)b * a.Hq + h) * S + qi] = m + fast_log2(lt);
 }
 
-// dQ per query row; also delta = rowsum(dO * O) for the dK/dV kernel.
-__global__ __launch_bounds__(64 * kWaves) void attn_bwd_dq_f32(Args a) {
-  __shared__ float xs[kWaves][2][128];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t r = (int64_t)blockIdx.x * kWaves + wave;
-  if (r >= (int64_t)a.B * a.Hq * a.S) return;  // wave-uniform; no barrier below
-  int b, h, i;
-  split_row(r, a.Hq, a.S, b, h, i);
+// ---------------------------------------------------------------- dQ (+ delta)
+// Head dims 64 and 128 keep Q, dO, dQ^T and the staged tiles at one wave per
+// SIMD (head dim 64 spills at two).
+template <int DP>
+__global__ __launch_bounds__(64 * kWaves)
+__attribute__((amdgpu_waves_per_eu(DP >= 64 ? 1 : 2, DP >= 64 ? 1 : 2)))
+void attn_bwd_dq_f32(Args a) {
+  constexpr int P = DP + 1, NS = DP / 2, NDB = DP / 32;
+  __shared__ float Ks[32 * P], Vs[32 * P];
+  __shared__ int64_t kd[32];
+  __shared__ Visit vis;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hh = lane >> 5, l32 = lane & 31;
+  const int S = a.S, D = a.D;
+  const int nqt = (S + kRows - 1) / kRows;
+  const int qt = nqt - 1 - (int)(blockIdx.x % nqt);
+  const int bh = (int)(blockIdx.x / nqt), h = bh % a.Hq, b = bh / a.Hq;
   const int hk = h / (a.Hq / a.Hkv);
-  const float sl2 = a.scale * kLog2e;
-  float *qx = xs[wave][0], *gx = xs[wave][1];
-  const float *qrow = a.q.row(b, h, i), *grow = a.dout.row(b, h, i), *orow = a.o.row(b, h, i);
-  float dl = 0.f;
-  for (int d = lane; d < a.D; d += 64) {
-    qx[d] = qrow[d] * sl2;
-    gx[d] = grow[d];
-    dl = fmaf(grow[d], orow[d], dl);
-  }
-  dl = wave_sum(dl);
-  const int64_t ri = ((int64_t)b * a.Hq + h) * a.S + i;
-  if (lane == 0) a.delta[ri] = dl;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  const float lse = a.lse[ri];
+  const bool vec = a.vec != 0;
   const int64_t *docb = a.doc + b * a.doc_sb;
-  const int64_t di = docb[i];
-  float q0 = 0.f, q1 = 0.f;
-  for (int j0 = 0; j0 <= i; j0 += 64) {
-    const int j = j0 + lane;
-    const bool ok = j <= i && docb[j <= i ? j : i] == di;
-    if (__builtin_amdgcn_ballot_w64(ok) == 0) continue;
-    float ds = 0.f;
-    if (ok) {
-      const float p = fast_exp2(dot_row(qx, a.k.row(b, hk, j), a.D, a.vec) - lse);
-      ds = p * (dot_row(gx, a.v.row(b, hk, j), a.D, a.vec) - dl);
-    }
-    const int n = min(64, i + 1 - j0);
-    for (int t = 0; t < n; ++t) {
-      const float st = bcast(ds, t);
-      if (st == 0.f) continue;
-      const float *kr = a.k.row(b, hk, j0 + t);
-      if (lane < a.D) q0 = fmaf(st, kr[lane], q0);
-      if (lane + 64 < a.D) q1 = fmaf(st, kr[lane + 64], q1);
+  const float sl2 = a.scale * kLog2e;
+
+  const int qi = qt * kRows + wave * 32 + l32;
+  const bool qv = qi < S;
+  const int64_t qdoc = docb[qv ? qi : S - 1];
+  float qf[NS], gf[NS];  // Q (log2-scaled) and dO at columns 2k + hh
+  float dl = 0.f;
+  {
+    const float *qr = a.q.row(b, h, qv ? qi : 0), *gr = a.dout.row(b, h, qv ? qi : 0);
+    const float *orow = a.o.row(b, h, qv ? qi : 0);
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+      const bool in = qv && 2 * k + hh < D;
+      qf[k] = in ? qr[2 * k + hh] * sl2 : 0.f;
+      gf[k] = in ? gr[2 * k + hh] : 0.f;
+      dl = in ? fmaf(gf[k], orow[2 * k + hh], dl) : dl;
     }
   }
-  float *dqr = a.dq.row(b, h, i);
-  if (lane < a.D) dqr[lane] = q0 * a.scale;
-  if (lane + 64 < a.D) dqr[lane + 64] = q1 * a.scale;
+  dl += xor32(dl);  // delta_i = rowsum(dO_i * O_i)
+  const int64_t ri = ((int64_t)b * a.Hq + h) * S + (qv ? qi : 0);
+  if (qv && hh == 0) a.delta[ri] = dl;
+  const float lse = qv ? a.lse[ri] : 0.f;
+  f32x16_t dqacc[NDB];
+#pragma unroll
+  for (int i = 0; i < NDB; ++i) dqacc[i] = zero16();
+
+  // KV sub-tiles up to the causal bound that hold an allowed pair for some row
+  // of the workgroup.
+  const int kv_end = min(S, (qt + 1) * kRows);
+  const int nl = visit_list<true>(vis, docb, S, qt * kRows, 0, kv_end);
+  const int nst = nl >= 0 ? nl : (kv_end + 31) / 32;
+  auto tile_of = [&](int i) { return nl >= 0 ? vis.list[i] : i; };
+  Tile<DP> tk, tv;
+  int64_t dnext = 0;
+  auto fetch = [&](int st) {
+    tk.load(a.k, b, hk, 32 * st, S, D, vec);
+    tv.load(a.v, b, hk, 32 * st, S, D, vec);
+    if (tid < 32) dnext = 32 * st + tid < S ? docb[32 * st + tid] : 0;
+  };
+  if (nst > 0) fetch(tile_of(0));
+  for (int i = 0; i < nst; ++i) {
+    __syncthreads();  // every wave is done with the previous sub-tile
+    tk.store(Ks, vec);
+    tv.store(Vs, vec);
+    if (tid < 32) kd[tid] = dnext;
+    __syncthreads();
+    const int kv0 = 32 * tile_of(i);
+    if (i + 1 < nst) fetch(tile_of(i + 1));
+    unsigned okm = 0;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kv = kv0 + crow(hh, r);
+      okm |= (unsigned)(qv && kv <= qi && kd[crow(hh, r)] == qdoc) << r;
+    }
+    if (__builtin_amdgcn_ballot_w64(okm != 0) == 0) continue;
+    f32x16_t sacc = zero16(), pacc = zero16();
+#pragma unroll
+    for (int k = 0; k < NS; ++k)
+      if (2 * k < D) {
+        sacc = mfma(Ks[l32 * P + 2 * k + hh], qf[k], sacc);  // S^T = K Q^T
+        pacc = mfma(Vs[l32 * P + 2 * k + hh], gf[k], pacc);  // dP^T = V dO^T
+      }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float p = (okm >> r) & 1 ? fast_exp2(sacc[r] - lse) : 0.f;
+      sacc[r] = p * (pacc[r] - dl);  // dS^T
+    }
+    // dQ^T += K^T dS^T
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+      if (32 * db < D) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          dqacc[db] = mfma(Ks[crow(hh, r) * P + 32 * db + l32], sacc[r], dqacc[db]);
+      }
+  }
+  if (!qv) return;
+  float *dqr = a.dq.row(b, h, qi);
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int d = 32 * db + crow(hh, r);
+      if (d < D) dqr[d] = dqacc[db][r] * a.scale;
+    }
 }
 
-// dK, dV per key row, summed over the query heads of its GQA group.
-__global__ __launch_bounds__(64 * kWaves) void attn_bwd_dkdv_f32(Args a) {
-  __shared__ float xs[kWaves][2][128];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t r = (int64_t)blockIdx.x * kWaves + wave;
-  if (r >= (int64_t)a.B * a.Hkv * a.S) return;  // wave-uniform; no barrier below
-  int b, hk, j;
-  split_row(r, a.Hkv, a.S, b, hk, j);
+// ---------------------------------------------------------------- dK, dV
+// Head dims 64 and 128 keep K, V, dK^T, dV^T and the staged tiles at one wave
+// per SIMD (head dim 64 spills at two).
+template <int DP>
+__global__ __launch_bounds__(64 * kWaves)
+__attribute__((amdgpu_waves_per_eu(DP >= 64 ? 1 : 2, DP >= 64 ? 1 : 2)))
+void attn_bwd_dkdv_f32(Args a) {
+  constexpr int P = DP + 1, NS = DP / 2, NDB = DP / 32;
+  __shared__ float Qs[32 * P], Gs[32 * P];
+  __shared__ int64_t qd[32];
+  __shared__ float ls[32], dls[32];
+  __shared__ Visit vis;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hh = lane >> 5, l32 = lane & 31;
+  const int S = a.S, D = a.D;
   const int G = a.Hq / a.Hkv;
-  const float sl2 = a.scale * kLog2e;
-  float *kx = xs[wave][0], *vx = xs[wave][1];
-  const float *krow = a.k.row(b, hk, j), *vrow = a.v.row(b, hk, j);
-  for (int d = lane; d < a.D; d += 64) {
-    kx[d] = krow[d] * sl2;
-    vx[d] = vrow[d];
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int nkt = (S + kRows - 1) / kRows;
+  const int kt = (int)(blockIdx.x % nkt);
+  const int bh = (int)(blockIdx.x / nkt), hk = bh % a.Hkv, b = bh / a.Hkv;
+  const bool vec = a.vec != 0;
   const int64_t *docb = a.doc + b * a.doc_sb;
-  const int64_t dj = docb[j];
-  float k0 = 0.f, k1 = 0.f, v0 = 0.f, v1 = 0.f;
-  for (int g = 0; g < G; ++g) {
-    const int h = hk * G + g;
-    const float *lse = a.lse + ((int64_t)b * a.Hq + h) * a.S;
-    const float *dlt = a.delta + ((int64_t)b * a.Hq + h) * a.S;
-    for (int i0 = j; i0 < a.S; i0 += 64) {
-      const int i = i0 + lane;
-      const bool ok = i < a.S && docb[i < a.S ? i : a.S - 1] == dj;
-      if (__builtin_amdgcn_ballot_w64(ok) == 0) continue;
-      float p = 0.f, ds = 0.f;
-      if (ok) {
-        p = fast_exp2(dot_row(kx, a.q.row(b, h, i), a.D, a.vec) - lse[i]);
-        ds = p * (dot_row(vx, a.dout.row(b, h, i), a.D, a.vec) - dlt[i]);
-      }
-      const int n = min(64, a.S - i0);
-      for (int t = 0; t < n; ++t) {
-        const float pt = bcast(p, t), st = bcast(ds, t);
-        if (pt == 0.f && st == 0.f) continue;
-        const float *gr = a.dout.row(b, h, i0 + t), *qr = a.q.row(b, h, i0 + t);
-        if (lane < a.D) {
-          v0 = fmaf(pt, gr[lane], v0);
-          k0 = fmaf(st, qr[lane], k0);
-        }
-        if (lane + 64 < a.D) {
-          v1 = fmaf(pt, gr[lane + 64], v1);
-          k1 = fmaf(st, qr[lane + 64], k1);
-        }
-      }
+  const float sl2 = a.scale * kLog2e;
+
+  const int kv = kt * kRows + wave * 32 + l32;
+  const bool kvv = kv < S;
+  const int64_t kvdoc = docb[kvv ? kv : S - 1];
+  float kf[NS], vf[NS];  // B operands of S = Q K^T (K log2-scaled) and dP = dO V^T
+  {
+    const float *kr = a.k.row(b, hk, kvv ? kv : 0), *vr = a.v.row(b, hk, kvv ? kv : 0);
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+      const bool in = kvv && 2 * k + hh < D;
+      kf[k] = in ? kr[2 * k + hh] * sl2 : 0.f;
+      vf[k] = in ? vr[2 * k + hh] : 0.f;
     }
   }
-  float *dkr = a.dk.row(b, hk, j), *dvr = a.dv.row(b, hk, j);
-  if (lane < a.D) {
-    dkr[lane] = k0 * a.scale;
-    dvr[lane] = v0;
+  f32x16_t dkacc[NDB], dvacc[NDB];
+#pragma unroll
+  for (int i = 0; i < NDB; ++i) {
+    dkacc[i] = zero16();
+    dvacc[i] = zero16();
   }
-  if (lane + 64 < a.D) {
-    dkr[lane + 64] = k1 * a.scale;
-    dvr[lane + 64] = v1;
+
+  // Steps t = (query head g of the group, listed 32-row query sub-tile): the
+  // sub-tiles at or after the workgroup's first KV row that hold an allowed
+  // pair for some of its rows (the same for every head of the group).
+  const int st0 = (kt * kRows) / 32;
+  const int nl = visit_list<false>(vis, docb, S, kt * kRows, kt * kRows, S);
+  const int nq = nl >= 0 ? nl : (S + 31) / 32 - st0;
+  auto tile_of = [&](int i) { return nl >= 0 ? vis.list[i] : st0 + i; };
+  const int T = G * nq;
+  Tile<DP> tq, tg;
+  int64_t dnext = 0;
+  float lnext = 0.f;
+  auto fetch = [&](int t) {
+    const int g = t / nq, st = tile_of(t - (t / nq) * nq), h = hk * G + g;
+    tq.load(a.q, b, h, 32 * st, S, D, vec);
+    tg.load(a.dout, b, h, 32 * st, S, D, vec);
+    if (tid < 32) {
+      const int q = 32 * st + tid;
+      dnext = q < S ? docb[q] : 0;
+    } else if (tid < 96) {  // lse (threads 32..63) and delta (64..95) of the sub-tile's rows
+      const int q = 32 * st + (tid & 31);
+      const int64_t ri = ((int64_t)b * a.Hq + h) * S + q;
+      lnext = q < S ? (tid < 64 ? a.lse[ri] : a.delta[ri]) : 0.f;
+    }
+  };
+  if (T > 0) fetch(0);
+  for (int t = 0; t < T; ++t) {
+    __syncthreads();
+    tq.store(Qs, vec);
+    tg.store(Gs, vec);
+    if (tid < 32) qd[tid] = dnext;
+    else if (tid < 64) ls[tid - 32] = lnext;
+    else if (tid < 96) dls[tid - 64] = lnext;
+    __syncthreads();
+    const int q0 = 32 * tile_of(t % nq);
+    if (t + 1 < T) fetch(t + 1);
+    unsigned okm = 0;  // bit r: pair (query q0 + crow(hh, r), KV row kv) allowed
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int q = q0 + crow(hh, r);
+      okm |= (unsigned)(kvv && q < S && q >= kv && qd[crow(hh, r)] == kvdoc) << r;
+    }
+    if (__builtin_amdgcn_ballot_w64(okm != 0) == 0) continue;
+    f32x16_t sacc = zero16(), pacc = zero16();
+#pragma unroll
+    for (int k = 0; k < NS; ++k)
+      if (2 * k < D) {
+        sacc = mfma(Qs[l32 * P + 2 * k + hh], kf[k], sacc);  // S = Q K^T (lane <-> KV column)
+        pacc = mfma(Gs[l32 * P + 2 * k + hh], vf[k], pacc);  // dP = dO V^T
+      }
+    float pv[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int qr = crow(hh, r);
+      const float p = (okm >> r) & 1 ? fast_exp2(sacc[r] - ls[qr]) : 0.f;
+      pv[r] = p;
+      sacc[r] = p * (pacc[r] - dls[qr]);  // dS
+    }
+    // dV^T += dO^T P, dK^T += Q^T dS (step r pairs query rows crow(0, r), crow(1, r))
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+      if (32 * db < D) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          dvacc[db] = mfma(Gs[crow(hh, r) * P + 32 * db + l32], pv[r], dvacc[db]);
+          dkacc[db] = mfma(Qs[crow(hh, r) * P + 32 * db + l32], sacc[r], dkacc[db]);
+        }
+      }
   }
+  if (!kvv) return;
+  float *dkr = a.dk.row(b, hk, kv), *dvr = a.dv.row(b, hk, kv);
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int d = 32 * db + crow(hh, r);
+      if (d < D) {
+        dkr[d] = dkacc[db][r] * a.scale;
+        dvr[d] = dvacc[db][r];
+      }
+    }
 }
 
 View view_of(const pb_bhsd *t) {
@@ -246,7 +550,8 @@ int check(const char *what, int64_t b, int64_t hq, int64_t hkv, int64_t s, int64
   PB_CHECK_ARG(hq % hkv == 0, "%s: query heads (%lld) not a multiple of kv heads (%lld)", what,
                (long long)hq, (long long)hkv);
   PB_CHECK_SUPPORTED(d <= 128, "%s: head_dim %lld > 128 is not supported", what, (long long)d);
-  PB_CHECK_SUPPORTED(s < (1LL << 30) && b * hq * s / kWaves < (1LL << 31),
+  PB_CHECK_SUPPORTED(s < (1LL << 30) && b * hq * ((s + kRows - 1) / kRows) < (1LL << 31) &&
+                         b * hq * s < (1LL << 40),
                      "%s: problem too large", what);
   return PB_OK;
 }
@@ -274,9 +579,11 @@ extern "C" int pb_attn_fwd_f32(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd
   a.B = (int)b; a.Hq = (int)hq; a.Hkv = (int)hkv; a.S = (int)s; a.D = (int)d;
   a.scale = scale;
   a.vec = d % 4 == 0 && rows_aligned(k) && rows_aligned(v);
-  const int64_t rows = b * hq * s;
-  hipLaunchKernelGGL(attn_fwd_f32, dim3((unsigned)((rows + kWaves - 1) / kWaves)),
-                     dim3(64 * kWaves), 0, as_stream(stream), a);
+  const dim3 grid((unsigned)(b * hq * ((s + kRows - 1) / kRows))), block(64 * kWaves);
+  hipStream_t st = as_stream(stream);
+  if (d <= 32) hipLaunchKernelGGL(attn_fwd_f32<32>, grid, block, 0, st, a);
+  else if (d <= 64) hipLaunchKernelGGL(attn_fwd_f32<64>, grid, block, 0, st, a);
+  else hipLaunchKernelGGL(attn_fwd_f32<128>, grid, block, 0, st, a);
   return launch_status("pb_attn_fwd_f32");
 }
 
@@ -305,12 +612,16 @@ extern "C" int pb_attn_bwd_f32(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd
   a.vec = d % 4 == 0 && rows_aligned(q) && rows_aligned(k) && rows_aligned(v) &&
           rows_aligned(dout);
   hipStream_t st = as_stream(stream);
-  const int64_t qrows = b * hq * s, kvrows = b * hkv * s;
-  hipLaunchKernelGGL(attn_bwd_dq_f32, dim3((unsigned)((qrows + kWaves - 1) / kWaves)),
-                     dim3(64 * kWaves), 0, st, a);
+  const int64_t tiles = (s + kRows - 1) / kRows;
+  const dim3 gq((unsigned)(b * hq * tiles)), gkv((unsigned)(b * hkv * tiles)), block(64 * kWaves);
+  // dQ first: it writes delta, which the dK/dV kernel reads.
+  if (d <= 32) hipLaunchKernelGGL(attn_bwd_dq_f32<32>, gq, block, 0, st, a);
+  else if (d <= 64) hipLaunchKernelGGL(attn_bwd_dq_f32<64>, gq, block, 0, st, a);
+  else hipLaunchKernelGGL(attn_bwd_dq_f32<128>, gq, block, 0, st, a);
   rc = launch_status("pb_attn_bwd_f32(dq)");
   if (rc) return rc;
-  hipLaunchKernelGGL(attn_bwd_dkdv_f32, dim3((unsigned)((kvrows + kWaves - 1) / kWaves)),
-                     dim3(64 * kWaves), 0, st, a);
+  if (d <= 32) hipLaunchKernelGGL(attn_bwd_dkdv_f32<32>, gkv, block, 0, st, a);
+  else if (d <= 64) hipLaunchKernelGGL(attn_bwd_dkdv_f32<64>, gkv, block, 0, st, a);
+  else hipLaunchKernelGGL(attn_bwd_dkdv_f32<128>, gkv, block, 0, st, a);
   return launch_status("pb_attn_bwd_f32(dkdv)");
 }
