@@ -429,7 +429,8 @@ def attention_f32_kernels(dev, iters: int) -> dict:
     dk = torch.empty(B, S, Hkv, D, device=dev).transpose(1, 2)
     dv = torch.empty_like(dk)
     lse = torch.empty(B, Hq, S, device=dev)
-    delta = torch.empty(B, Hq, S, device=dev)
+    bws = torch.empty(N.lib().pb_attn_bwd_f32_workspace_bytes(B, Hq, Hkv, S, D),
+                      dtype=torch.uint8, device=dev)
     sc, st = 1.0 / D ** 0.5, N.stream_ptr(q)
 
     def fwd():
@@ -439,7 +440,7 @@ def attention_f32_kernels(dev, iters: int) -> dict:
     def bwd():
         N.call("pb_attn_bwd_f32", N.BHSD.of(q), N.BHSD.of(k), N.BHSD.of(v), N.BHSD.of(out),
                N.BHSD.of(do), N.BHSD.of(dq), N.BHSD.of(dk), N.BHSD.of(dv), lse.data_ptr(),
-               delta.data_ptr(), doc.data_ptr(), doc.stride(0), B, Hq, Hkv, S, D, sc, st)
+               bws.data_ptr(), doc.data_ptr(), doc.stride(0), B, Hq, Hkv, S, D, sc, st)
 
     fwd()
     bwd()
@@ -454,9 +455,8 @@ def attention_f32_kernels(dev, iters: int) -> dict:
         "fwd_ms": t_f, "bwd_ms": t_b,
         "fwd_bwd_tflops": (f_fwd + f_bwd) / (t_f + t_b) / 1e9,
         "frac_fp32_peak": (f_fwd + f_bwd) / (t_f + t_b) / 1e9 / PEAK_FP32_TFLOPS,
-        "note": "precision path (pb_attn_fwd_f32 / pb_attn_bwd_f32): fp32 MFMA, one workgroup "
-                "per 128-row tile walks its whole KV (or query) list, so the longest document "
-                "sets the time; fraction of the 157.3 TFLOP/s dense fp32 peak",
+        "note": "precision path (pb_attn_fwd_f32 / pb_attn_bwd_f32): fp32 operands on the fp32 "
+                "matrix cores; fraction of the 157.3 TFLOP/s dense fp32 peak",
     }
 
 

@@ -225,19 +225,24 @@ int pb_attn_bwd(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v, const pb_b
  * non-autocast path, packbalance/model/attention.py:116-122, which computes
  * in fp32 where pb_attn_fwd takes bf16 operands).  Same mask, GQA mapping,
  * scale and log2-domain lse as pb_attn_fwd; q/k/v/out are fp32 pb_bhsd views
- * with unit head-dim stride, head_dim d <= 128; no plans or workspace.      */
+ * with unit head-dim stride, head_dim d <= 128; no plans or workspace.  fp32
+ * operands on the fp32 matrix cores.                                        */
 int pb_attn_fwd_f32(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v, const pb_bhsd *out,
                     float *lse, const int64_t *doc_ids, int64_t doc_stride, int64_t b,
                     int64_t hq, int64_t hkv, int64_t s, int64_t d, float scale, void *stream);
 
 /* Backward of pb_attn_fwd_f32 (FlexAttention's backward on fp32 tensors):
- * dQ, and dK / dV summed over each GQA group, all fp32.  delta: fp32
- * [b, hq, s] scratch (rowsum(dO * O)).                                      */
+ * dQ, and dK / dV summed over each GQA group, all fp32.  `workspace`:
+ * pb_attn_bwd_f32_workspace_bytes bytes, 256-byte aligned: delta =
+ * rowsum(dO * O), then on small grids the fp32 dK / dV partials of the KV
+ * tiles' chunked walks over heads and query sub-tiles, added in a fixed
+ * order (run-to-run deterministic).                                         */
+int64_t pb_attn_bwd_f32_workspace_bytes(int64_t b, int64_t hq, int64_t hkv, int64_t s, int64_t d);
 int pb_attn_bwd_f32(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v, const pb_bhsd *out,
                     const pb_bhsd *dout, const pb_bhsd *dq, const pb_bhsd *dk,
-                    const pb_bhsd *dv, const float *lse, float *delta, const int64_t *doc_ids,
-                    int64_t doc_stride, int64_t b, int64_t hq, int64_t hkv, int64_t s,
-                    int64_t d, float scale, void *stream);
+                    const pb_bhsd *dv, const float *lse, void *workspace,
+                    const int64_t *doc_ids, int64_t doc_stride, int64_t b, int64_t hq,
+                    int64_t hkv, int64_t s, int64_t d, float scale, void *stream);
 
 /* ---- Fused LM-head cross-entropy ----------------------------------------
  * Replaces packbalance/kernels/fused_ce.py:143-217 (_FusedLinearCE /

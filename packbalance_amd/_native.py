@@ -88,6 +88,7 @@ SIGNATURES: dict[str, tuple] = {
         [_pv, _pv, _pv, _pv, _pv, _pv, _pv, _pv, _p, _p, _p, _i64, _p, _p, _p, _p,
          _i64, _i64, _i64, _i64, _i64, _f32, _i32, _p],
     ),
+    "pb_attn_bwd_f32_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64]),
     "pb_attn_fwd_f32": (
         _i32, [_pv, _pv, _pv, _pv, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _p],
     ),
@@ -157,7 +158,7 @@ SIGNATURES: dict[str, tuple] = {
     "pb_transpose_batched": (_i32, [_p, _i64, _i64, _p, _i64, _i64, _i64, _i32, _p]),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lib: C.CDLL | None = None
 _load_error: str | None = None

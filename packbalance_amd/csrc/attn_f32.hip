@@ -31,6 +31,8 @@
 // position of the other axis, visit_list) and loads only those; a wave then
 // skips a listed sub-tile whose 32 x 32 pairs hold none for its own rows.  So
 // the work follows the documents, and nothing past the causal bound is read.
+#include <type_traits>
+
 #include "attn_common.hpp"
 
 namespace pb {
@@ -53,7 +55,28 @@ struct Args {
   int B, Hq, Hkv, S, D;
   float scale;  // softmax scale
   int vec;      // K / V / Q / dO rows may be read as float4 (D % 4 == 0, 16-byte aligned rows)
+  // dK/dV step chunking on small grids: a KV tile's steps (heads x listed
+  // query sub-tiles) are cut into at most nsplit chunks of at least
+  // kMinChunk steps, one workgroup each (chunk index = blockIdx.x / tiles).  A
+  // tile with more than one chunk leaves per-chunk fp32 dK and dV rows (D
+  // floats) at part / part2 (+ c * pstride) that attn_f32_sum_chunks adds up;
+  // nch[tile] = its chunk count.
+  int nsplit;
+  int *nch;
+  float *part, *part2;
+  int64_t pstride;
 };
+
+constexpr int kMinChunk = 4;
+
+// Chunk c of a list of n >= 1 entries: [i0, i1) and the tile's chunk count.
+__device__ __forceinline__ void chunk_of(int n, int nsplit, int c, int &i0, int &i1, int &nch) {
+  int ch = (n + nsplit - 1) / nsplit;
+  if (ch < kMinChunk) ch = kMinChunk;
+  nch = (n + ch - 1) / ch;
+  i0 = c * ch;
+  i1 = min(n, i0 + ch);
+}
 
 using attn::f32x16_t;
 using attn::zero16;
@@ -240,7 +263,7 @@ void attn_fwd_f32(Args a) {
     tv.load(a.v, b, hk, 32 * st, S, D, vec);
     if (tid < 32) dnext = 32 * st + tid < S ? docb[32 * st + tid] : 0;
   };
-  if (nst > 0) fetch(tile_of(0));
+  fetch(tile_of(0));  // nst >= 1: row qi always sees itself
   for (int i = 0; i < nst; ++i) {
     __syncthreads();  // every wave is done with the previous sub-tile
     tk.store(Ks, vec);
@@ -290,7 +313,7 @@ void attn_fwd_f32(Args a) {
   }
   const float lt = l + xor32(l);
   if (!qv) return;
-  const float inv = lt > 0.f ? 1.0f / lt : 0.f;  // lt >= 1: row qi always sees itself
+  const float inv = 1.0f / lt;  // lt >= 1: row qi always sees itself
   float *orow = a.o.row(b, h, qi);
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
@@ -299,7 +322,7 @@ void attn_fwd_f32(Args a) {
       const int d = 32 * db + crow(hh, r);
       if (d < D) orow[d] = oacc[db][r] * inv;
     }
-  if (hh == 0) a.lse[((int64_t)b * a.Hq + h) * S + qi] = m + fast_log2(lt);
+  if (hh == 0) a.lse[(int64_t)bh * S + qi] = m + fast_log2(lt);
 }
 
 // ---------------------------------------------------------------- dQ (+ delta)
@@ -361,7 +384,7 @@ void attn_bwd_dq_f32(Args a) {
     tv.load(a.v, b, hk, 32 * st, S, D, vec);
     if (tid < 32) dnext = 32 * st + tid < S ? docb[32 * st + tid] : 0;
   };
-  if (nst > 0) fetch(tile_of(0));
+  fetch(tile_of(0));  // nst >= 1: row qi always sees itself
   for (int i = 0; i < nst; ++i) {
     __syncthreads();  // every wave is done with the previous sub-tile
     tk.store(Ks, vec);
@@ -426,8 +449,10 @@ void attn_bwd_dkdv_f32(Args a) {
   const int S = a.S, D = a.D;
   const int G = a.Hq / a.Hkv;
   const int nkt = (S + kRows - 1) / kRows;
-  const int kt = (int)(blockIdx.x % nkt);
-  const int bh = (int)(blockIdx.x / nkt), hk = bh % a.Hkv, b = bh / a.Hkv;
+  const int tiles = a.B * a.Hkv * nkt;
+  const int chunk = (int)blockIdx.x / tiles, tb = (int)blockIdx.x - chunk * tiles;
+  const int kt = tb % nkt;
+  const int bh = tb / nkt, hk = bh % a.Hkv, b = bh / a.Hkv;
   const bool vec = a.vec != 0;
   const int64_t *docb = a.doc + b * a.doc_sb;
   const float sl2 = a.scale * kLog2e;
@@ -460,6 +485,10 @@ void attn_bwd_dkdv_f32(Args a) {
   const int nq = nl >= 0 ? nl : (S + 31) / 32 - st0;
   auto tile_of = [&](int i) { return nl >= 0 ? vis.list[i] : st0 + i; };
   const int T = G * nq;
+  int i0, i1, nch;  // this workgroup's steps [i0, i1) of the T
+  chunk_of(T, a.nsplit, chunk, i0, i1, nch);
+  if (i0 >= i1) return;  // uniform: an empty chunk slot
+  if (chunk == 0 && tid == 0 && a.nsplit > 1) a.nch[bh * nkt + kt] = nch;
   Tile<DP> tq, tg;
   int64_t dnext = 0;
   float lnext = 0.f;
@@ -476,8 +505,8 @@ void attn_bwd_dkdv_f32(Args a) {
       lnext = q < S ? (tid < 64 ? a.lse[ri] : a.delta[ri]) : 0.f;
     }
   };
-  if (T > 0) fetch(0);
-  for (int t = 0; t < T; ++t) {
+  fetch(i0);
+  for (int t = i0; t < i1; ++t) {
     __syncthreads();
     tq.store(Qs, vec);
     tg.store(Gs, vec);
@@ -486,7 +515,7 @@ void attn_bwd_dkdv_f32(Args a) {
     else if (tid < 96) dls[tid - 64] = lnext;
     __syncthreads();
     const int q0 = 32 * tile_of(t % nq);
-    if (t + 1 < T) fetch(t + 1);
+    if (t + 1 < i1) fetch(t + 1);
     unsigned okm = 0;  // bit r: pair (query q0 + crow(hh, r), KV row kv) allowed
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -521,7 +550,9 @@ void attn_bwd_dkdv_f32(Args a) {
       }
   }
   if (!kvv) return;
-  float *dkr = a.dk.row(b, hk, kv), *dvr = a.dv.row(b, hk, kv);
+  const int64_t ro = ((int64_t)bh * S + kv) * D + chunk * a.pstride;
+  float *dkr = nch == 1 ? a.dk.row(b, hk, kv) : a.part + ro;
+  float *dvr = nch == 1 ? a.dv.row(b, hk, kv) : a.part2 + ro;
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -532,6 +563,30 @@ void attn_bwd_dkdv_f32(Args a) {
         dvr[d] = dvacc[db][r];
       }
     }
+}
+
+// dK / dV of KV tiles with more than one chunk: the chunk partials added in
+// chunk order (run-to-run deterministic), one thread per output element.
+__global__ __launch_bounds__(256) void attn_f32_sum_chunks(Args a) {
+  const int heads = a.Hkv;
+  const int64_t rows = (int64_t)a.B * heads * a.S;
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= rows * a.D) return;
+  const int64_t row = e / a.D;
+  const int d = (int)(e - row * a.D);
+  const int S = a.S;
+  const int q = (int)(row % S), bh = (int)(row / S);
+  const int nt = (S + kRows - 1) / kRows;
+  const int nch = a.nch[bh * nt + q / kRows];
+  if (nch <= 1) return;
+  const int b = bh / heads, hh = bh % heads;
+  float s0 = 0.f, s1 = 0.f;
+  for (int c = 0; c < nch; ++c) {
+    s0 += a.part[c * a.pstride + e];
+    s1 += a.part2[c * a.pstride + e];
+  }
+  a.dk.row(b, hh, q)[d] = s0;
+  a.dv.row(b, hh, q)[d] = s1;
 }
 
 View view_of(const pb_bhsd *t) {
@@ -556,10 +611,50 @@ int check(const char *what, int64_t b, int64_t hq, int64_t hkv, int64_t s, int64
   return PB_OK;
 }
 
+// Chunks per tile for a grid of `tiles` workgroups: split only small grids,
+// aiming at ~2048 workgroups (at most 8 chunks).
+inline int splits_for(int64_t tiles) {
+  if (tiles >= 1024) return 1;
+  const int64_t n = (2048 + tiles - 1) / tiles;
+  return (int)(n < 8 ? n : 8);
+}
+
+inline int64_t al256(int64_t bytes) { return (bytes + 255) / 256 * 256; }
+
+// Workspace of pb_attn_bwd_f32: delta [B*Hq*S], then (dK/dV grid split)
+// nch [KV tiles] int and the dK and dV partials [nsplit][B*Hkv*S][D] each.
+struct Layout {
+  int nsplit;
+  int64_t nch, part_k, part_v, total;
+};
+
+inline Layout bwd_layout(int64_t b, int64_t hq, int64_t hkv, int64_t s, int64_t d) {
+  Layout L = {};
+  const int64_t nt = (s + kRows - 1) / kRows, kvrows = b * hkv * s;
+  L.nsplit = splits_for(b * hkv * nt);
+  int64_t off = al256(b * hq * s * 4);  // delta
+  if (L.nsplit > 1) {
+    L.nch = off;
+    off += al256(b * hkv * nt * 4);
+    L.part_k = off;
+    off += al256(L.nsplit * kvrows * d * 4);
+    L.part_v = off;
+    off += al256(L.nsplit * kvrows * d * 4);
+  }
+  L.total = off;
+  return L;
+}
+
 }  // namespace attn32
 }  // namespace pb
 
 using pb::attn32::Args;
+
+extern "C" int64_t pb_attn_bwd_f32_workspace_bytes(int64_t b, int64_t hq, int64_t hkv, int64_t s,
+                                                    int64_t d) {
+  if (b < 1 || hq < 1 || hkv < 1 || s < 1 || d < 1) return 0;
+  return pb::attn32::bwd_layout(b, hq, hkv, s, d).total;
+}
 
 extern "C" int pb_attn_fwd_f32(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v,
                                const pb_bhsd *out, float *lse, const int64_t *doc_ids,
@@ -590,7 +685,7 @@ extern "C" int pb_attn_fwd_f32(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd
 extern "C" int pb_attn_bwd_f32(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd *v,
                                const pb_bhsd *out, const pb_bhsd *dout, const pb_bhsd *dq,
                                const pb_bhsd *dk, const pb_bhsd *dv, const float *lse,
-                               float *delta, const int64_t *doc_ids, int64_t doc_stride,
+                               void *workspace, const int64_t *doc_ids, int64_t doc_stride,
                                int64_t b, int64_t hq, int64_t hkv, int64_t s, int64_t d,
                                float scale, void *stream) {
   using namespace pb;
@@ -598,30 +693,46 @@ extern "C" int pb_attn_bwd_f32(const pb_bhsd *q, const pb_bhsd *k, const pb_bhsd
   clear_error();
   int rc = check("pb_attn_bwd_f32", b, hq, hkv, s, d);
   if (rc) return rc;
-  PB_CHECK_ARG(q && k && v && out && dout && dq && dk && dv && lse && delta && doc_ids,
+  PB_CHECK_ARG(q && k && v && out && dout && dq && dk && dv && lse && workspace && doc_ids,
                "pb_attn_bwd_f32: null argument");
   PB_CHECK_ARG(scale > 0.f, "pb_attn_bwd_f32: softmax scale must be positive");
+  const Layout L = bwd_layout(b, hq, hkv, s, d);
+  char *ws = static_cast<char *>(workspace);
   Args a = {};
   a.q = view_of(q); a.k = view_of(k); a.v = view_of(v); a.o = view_of(out);
   a.dout = view_of(dout); a.dq = view_of(dq); a.dk = view_of(dk); a.dv = view_of(dv);
   a.lse = const_cast<float *>(lse);
-  a.delta = delta;
+  a.delta = reinterpret_cast<float *>(ws);
   a.doc = doc_ids; a.doc_sb = doc_stride;
   a.B = (int)b; a.Hq = (int)hq; a.Hkv = (int)hkv; a.S = (int)s; a.D = (int)d;
   a.scale = scale;
   a.vec = d % 4 == 0 && rows_aligned(q) && rows_aligned(k) && rows_aligned(v) &&
           rows_aligned(dout);
   hipStream_t st = as_stream(stream);
-  const int64_t tiles = (s + kRows - 1) / kRows;
-  const dim3 gq((unsigned)(b * hq * tiles)), gkv((unsigned)(b * hkv * tiles)), block(64 * kWaves);
+  const int64_t nt = (s + kRows - 1) / kRows;
+  const dim3 block(64 * kWaves);
   // dQ first: it writes delta, which the dK/dV kernel reads.
+  const dim3 gq((unsigned)(b * hq * nt));
   if (d <= 32) hipLaunchKernelGGL(attn_bwd_dq_f32<32>, gq, block, 0, st, a);
   else if (d <= 64) hipLaunchKernelGGL(attn_bwd_dq_f32<64>, gq, block, 0, st, a);
   else hipLaunchKernelGGL(attn_bwd_dq_f32<128>, gq, block, 0, st, a);
   rc = launch_status("pb_attn_bwd_f32(dq)");
   if (rc) return rc;
-  if (d <= 32) hipLaunchKernelGGL(attn_bwd_dkdv_f32<32>, gkv, block, 0, st, a);
-  else if (d <= 64) hipLaunchKernelGGL(attn_bwd_dkdv_f32<64>, gkv, block, 0, st, a);
-  else hipLaunchKernelGGL(attn_bwd_dkdv_f32<128>, gkv, block, 0, st, a);
-  return launch_status("pb_attn_bwd_f32(dkdv)");
+  Args akv = a;
+  akv.nsplit = L.nsplit;
+  if (akv.nsplit > 1) {
+    akv.nch = reinterpret_cast<int *>(ws + L.nch);
+    akv.part = reinterpret_cast<float *>(ws + L.part_k);
+    akv.part2 = reinterpret_cast<float *>(ws + L.part_v);
+    akv.pstride = b * hkv * s * d;
+  }
+  const dim3 gkv((unsigned)(b * hkv * nt * akv.nsplit));
+  if (d <= 32) hipLaunchKernelGGL(attn_bwd_dkdv_f32<32>, gkv, block, 0, st, akv);
+  else if (d <= 64) hipLaunchKernelGGL(attn_bwd_dkdv_f32<64>, gkv, block, 0, st, akv);
+  else hipLaunchKernelGGL(attn_bwd_dkdv_f32<128>, gkv, block, 0, st, akv);
+  rc = launch_status("pb_attn_bwd_f32(dkdv)");
+  if (rc || akv.nsplit == 1) return rc;
+  hipLaunchKernelGGL(attn_f32_sum_chunks, dim3((unsigned)((b * hkv * s * d + 255) / 256)), dim3(256),
+                     0, st, akv);
+  return launch_status("pb_attn_bwd_f32(dkdv sum)");
 }

@@ -32,4 +32,4 @@ int launch_status(const char *what) {
 
 extern "C" const char *pb_last_error(void) { return pb::g_msg; }
 
-extern "C" int pb_abi_version(void) { return 3; }
+extern "C" int pb_abi_version(void) { return 4; }

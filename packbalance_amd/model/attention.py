@@ -276,10 +276,11 @@ class _DocAttentionF32(torch.autograd.Function):
         dq = torch.empty((B, S, Hq, D), dtype=torch.float32, device=q.device).transpose(1, 2)
         dk = torch.empty((B, S, Hkv, D), dtype=torch.float32, device=q.device).transpose(1, 2)
         dv = torch.empty((B, S, Hkv, D), dtype=torch.float32, device=q.device).transpose(1, 2)
-        delta = torch.empty((B, Hq, S), dtype=torch.float32, device=q.device)
+        ws = torch.empty(N.lib().pb_attn_bwd_f32_workspace_bytes(B, Hq, Hkv, S, D),
+                         dtype=torch.uint8, device=q.device)
         N.call("pb_attn_bwd_f32", N.BHSD.of(q), N.BHSD.of(k), N.BHSD.of(v), N.BHSD.of(out),
                N.BHSD.of(g), N.BHSD.of(dq), N.BHSD.of(dk), N.BHSD.of(dv), lse.data_ptr(),
-               delta.data_ptr(), doc.data_ptr(), doc.stride(0), B, Hq, Hkv, S, D,
+               ws.data_ptr(), doc.data_ptr(), doc.stride(0), B, Hq, Hkv, S, D,
                float(ctx.scale), N.stream_ptr(q))
         return dq, dk, dv, None, None
 
