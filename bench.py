@@ -512,6 +512,51 @@ def lmhead_ce_kernels(dev, iters: int, vchunk: int = 8192, stored: bool = False)
     }
 
 
+def lmhead_ce_f32_kernels(dev, iters: int) -> dict:
+    """The fp32 LM-head CE path (fp32 x and W outside bf16 autocast, where the reference
+    computes fp32 logits): cfg4's shape with fp32 operands.  Labelled, not a headline:
+    fp32 library GEMMs (torch -> hipBLASLt) over token-row chunks of fp32 logits
+    (<= 1 GiB each) with the row CE kernel; fraction of the fp32 peak."""
+    import torch
+
+    from packbalance_amd.kernels.fused_ce import linear_cross_entropy
+
+    Nt, V, D = 16384, 128256, 4096
+    torch.manual_seed(0)
+    x = torch.randn(Nt, D, device=dev).requires_grad_(True)
+    w = (torch.randn(V, D, device=dev) * 0.02).requires_grad_(True)
+    t = torch.randint(0, V, (Nt,), device=dev)
+    t[torch.rand(Nt, device=dev) < 0.01] = -100
+    holder = {}
+
+    def fwd():
+        holder["loss"] = linear_cross_entropy(x, w, t)
+
+    def bwd():
+        holder["loss"].backward()
+
+    fwd()
+    bwd()
+    torch.cuda.synchronize()
+    tf = tb = 0.0
+    for _ in range(iters):
+        x.grad = None
+        w.grad = None
+        tf += events_ms(fwd, 1)
+        tb += events_ms(bwd, 1)
+    tf /= iters
+    tb /= iters
+    flops = 6.0 * Nt * V * D
+    return {
+        "workload": "cfg4 shape in fp32: x [16384, 4096], W [128256, 4096] fp32, 1% ignored",
+        "fwd_ms": tf, "bwd_ms": tb,
+        "tflops": flops / (tf + tb) / 1e9,
+        "frac_fp32_peak": flops / (tf + tb) / 1e9 / PEAK_FP32_TFLOPS,
+        "note": "precision path: fp32 logits GEMM per token-row chunk, row CE kernel, fp32 "
+                "dx / dW GEMMs (6NVD counted); fraction of the 157.3 TFLOP/s dense fp32 peak",
+    }
+
+
 def ce_rows_kernel(dev, iters: int, flush) -> dict:
     import torch
 
@@ -664,7 +709,7 @@ def main() -> int:
     ap.add_argument("--streams", type=int, default=2,
                     help="streams the step's micro-batches run on concurrently (1: one after another)")
     ap.add_argument("--only", choices=["train", "attention", "attention_cfg2", "attention_f32",
-                                       "lmhead_ce",
+                                       "lmhead_ce", "lmhead_ce_f32",
                                        "lmhead_ce_stored",
                                        "ce_rows", "norm_act", "copy", "peaks"],
                     default=None, help="run one part only (for profiling)")
@@ -692,6 +737,7 @@ def main() -> int:
               "attention_cfg2": lambda: attention_cfg2_kernels(dev, max(20, args.kernel_iters)),
               "attention_f32": lambda: attention_f32_kernels(dev, args.kernel_iters),
               "lmhead_ce": lambda: lmhead_ce_kernels(dev, args.kernel_iters),
+              "lmhead_ce_f32": lambda: lmhead_ce_f32_kernels(dev, 2),
               "lmhead_ce_stored": lambda: lmhead_ce_kernels(dev, args.kernel_iters, stored=True),
               "ce_rows": lambda: ce_rows_kernel(dev, args.kernel_iters, flush),
               "norm_act": lambda: norm_act_kernels(dev, args.kernel_iters, flush),
@@ -743,6 +789,8 @@ def main() -> int:
                                                             32768)
         kernels["lmhead_ce_chunk32768"]["note"] = ("variant: the default budget rule's chunk; "
                                                    "the configuration states 8192")
+        log("kernels: LM-head CE, fp32 path (cfg4 shape, labelled)")
+        kernels["lmhead_ce_f32"] = lmhead_ce_f32_kernels(dev, 2)
         log("kernels: row CE chunk")
         kernels["ce_rows"] = ce_rows_kernel(dev, args.kernel_iters, flush)
         log("kernels: RMSNorm / SwiGLU (cfg5)")
