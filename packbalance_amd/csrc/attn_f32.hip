@@ -24,8 +24,10 @@
 //                 head of the GQA group and every 32-row query sub-tile at or
 //                 after its rows: S = Q K^T and dP = dO V^T (lane <-> KV
 //                 column), then dV^T += dO^T P and dK^T += Q^T dS.
-// K / V (or Q / dO) sub-tiles pass through LDS (row pitch DP + 1 floats),
-// staged in registers one sub-tile ahead; the head dim is padded to DP (32,
+// K / V (or Q / dO) sub-tiles pass through LDS, staged in registers one
+// sub-tile ahead, in the layout each product reads as 16-byte vectors: row
+// split (a row's even then odd columns) for the A operand of S-type products,
+// transposed for that of PV-type products; the head dim is padded to DP (32,
 // 64 or 128) with zeros.  A workgroup first lists the sub-tiles that hold an
 // allowed pair for any of its rows (its rows' document runs against every
 // position of the other axis, visit_list) and loads only those; a wave then
@@ -93,6 +95,20 @@ __device__ __forceinline__ int crow(int h, int r) { return 8 * (r >> 2) + 4 * h 
 
 __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32); }
 
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// Lane (l32, h)'s A operands of an S-type product from a row-split tile:
+// k-steps 4q .. 4q + 3 (columns 2k + h of row l32).
+template <int DP>
+__device__ __forceinline__ f32x4_t rs4(const float *rs, int l32, int hh, int q) {
+  return *reinterpret_cast<const f32x4_t *>(rs + l32 * (DP + 4) + hh * (DP / 2) + 4 * q);
+}
+// Lane (l32, h)'s A operands of a PV-type product from a transposed tile: the
+// values of column 32 db + l32 at rows crow(h, 4g .. 4g + 3).
+__device__ __forceinline__ f32x4_t tr4(const float *tr, int db, int l32, int hh, int g) {
+  return *reinterpret_cast<const f32x4_t *>(tr + (32 * db + l32) * 36 + 8 * g + 4 * hh);
+}
+
 // A [32][DP] fp32 sub-tile (rows r0 .. r0 + 31 of one (pack, head) view,
 // columns past D and rows past S zero), staged in registers by the
 // workgroup's 256 threads and stored to LDS at pitch DP + 1.
@@ -124,22 +140,43 @@ struct Tile {
       }
     }
   }
-  __device__ __forceinline__ void store(float *lds, bool vec) const {
+  // (row, col) of the i-th value this thread holds.
+  __device__ __forceinline__ void at(int i, bool vec, int &row, int &col) const {
     const int tid = threadIdx.x;
     if (vec) {
-#pragma unroll
-      for (int i = 0; i < N / 4; ++i) {
-        const int e = tid + 64 * kWaves * i;
-        const int row = e / (DP / 4), col = (e % (DP / 4)) * 4;
-#pragma unroll
-        for (int x = 0; x < 4; ++x) lds[row * (DP + 1) + col + x] = v[4 * i + x];
-      }
+      const int e = tid + 64 * kWaves * (i / 4);
+      row = e / (DP / 4);
+      col = (e % (DP / 4)) * 4 + i % 4;
     } else {
+      const int e = tid + 64 * kWaves * i;
+      row = e / DP;
+      col = e % DP;
+    }
+  }
+  // Row-split layout (the A operand of S-type products, A[row][k = 2j + h]):
+  // row r at r * kRsPitch, its even columns then its odd ones, so lane half h
+  // reads its DP / 2 values of a row as contiguous 16-byte vectors.
+  static constexpr int kRsPitch = DP + 4;
+  static constexpr int kRsFloats = 32 * kRsPitch;
+  __device__ __forceinline__ void store_rs(float *lds, bool vec) const {
 #pragma unroll
-      for (int i = 0; i < N; ++i) {
-        const int e = tid + 64 * kWaves * i;
-        lds[(e / DP) * (DP + 1) + e % DP] = v[i];
-      }
+    for (int i = 0; i < N; ++i) {
+      int row, col;
+      at(i, vec, row, col);
+      lds[row * kRsPitch + (col & 1) * (DP / 2) + (col >> 1)] = v[i];
+    }
+  }
+  // Transposed layout (the A operand of PV-type products, A[d][k = row]):
+  // column c at c * kTrPitch, so a lane reads the rows crow(h, 4g .. 4g + 3)
+  // of its column as one 16-byte vector.
+  static constexpr int kTrPitch = 36;
+  static constexpr int kTrFloats = DP * kTrPitch;
+  __device__ __forceinline__ void store_tr(float *lds, bool vec) const {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      int row, col;
+      at(i, vec, row, col);
+      lds[col * kTrPitch + row] = v[i];
     }
   }
 };
@@ -221,8 +258,8 @@ template <int DP>
 __global__ __launch_bounds__(64 * kWaves)
 __attribute__((amdgpu_waves_per_eu(DP == 128 ? 1 : 2, DP == 128 ? 1 : 2)))
 void attn_fwd_f32(Args a) {
-  constexpr int P = DP + 1, NS = DP / 2, NDB = DP / 32;
-  __shared__ float Ks[32 * P], Vs[32 * P];
+  constexpr int NS = DP / 2, NDB = DP / 32;
+  __shared__ __align__(16) float Ks[Tile<DP>::kRsFloats], Vs[Tile<DP>::kTrFloats];
   __shared__ int64_t kd[32];
   __shared__ Visit vis;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -266,8 +303,8 @@ void attn_fwd_f32(Args a) {
   fetch(tile_of(0));  // nst >= 1: row qi always sees itself
   for (int i = 0; i < nst; ++i) {
     __syncthreads();  // every wave is done with the previous sub-tile
-    tk.store(Ks, vec);
-    tv.store(Vs, vec);
+    tk.store_rs(Ks, vec);
+    tv.store_tr(Vs, vec);
     if (tid < 32) kd[tid] = dnext;
     __syncthreads();
     const int kv0 = 32 * tile_of(i);
@@ -281,8 +318,12 @@ void attn_fwd_f32(Args a) {
     if (__builtin_amdgcn_ballot_w64(okm != 0) == 0) continue;  // uniform over the wave
     f32x16_t sacc = zero16();
 #pragma unroll
-    for (int k = 0; k < NS; ++k)
-      if (2 * k < D) sacc = mfma(Ks[l32 * P + 2 * k + hh], qf[k], sacc);
+    for (int q4 = 0; q4 < NS / 4; ++q4)
+      if (8 * q4 < D) {
+        const f32x4_t ka = rs4<DP>(Ks, l32, hh, q4);
+#pragma unroll
+        for (int x = 0; x < 4; ++x) sacc = mfma(ka[x], qf[4 * q4 + x], sacc);
+      }
     float mloc = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -307,8 +348,11 @@ void attn_fwd_f32(Args a) {
     for (int db = 0; db < NDB; ++db)
       if (32 * db < D) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          oacc[db] = mfma(Vs[crow(hh, r) * P + 32 * db + l32], sacc[r], oacc[db]);
+        for (int g = 0; g < 4; ++g) {
+          const f32x4_t va = tr4(Vs, db, l32, hh, g);
+#pragma unroll
+          for (int x = 0; x < 4; ++x) oacc[db] = mfma(va[x], sacc[4 * g + x], oacc[db]);
+        }
       }
   }
   const float lt = l + xor32(l);
@@ -332,8 +376,10 @@ template <int DP>
 __global__ __launch_bounds__(64 * kWaves)
 __attribute__((amdgpu_waves_per_eu(DP >= 64 ? 1 : 2, DP >= 64 ? 1 : 2)))
 void attn_bwd_dq_f32(Args a) {
-  constexpr int P = DP + 1, NS = DP / 2, NDB = DP / 32;
-  __shared__ float Ks[32 * P], Vs[32 * P];
+  constexpr int NS = DP / 2, NDB = DP / 32;
+  // K row-split (S^T) and transposed (dQ^T), V row-split (dP^T).
+  __shared__ __align__(16) float Ks[Tile<DP>::kRsFloats], Kt[Tile<DP>::kTrFloats];
+  __shared__ __align__(16) float Vs[Tile<DP>::kRsFloats];
   __shared__ int64_t kd[32];
   __shared__ Visit vis;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -387,8 +433,9 @@ void attn_bwd_dq_f32(Args a) {
   fetch(tile_of(0));  // nst >= 1: row qi always sees itself
   for (int i = 0; i < nst; ++i) {
     __syncthreads();  // every wave is done with the previous sub-tile
-    tk.store(Ks, vec);
-    tv.store(Vs, vec);
+    tk.store_rs(Ks, vec);
+    tk.store_tr(Kt, vec);
+    tv.store_rs(Vs, vec);
     if (tid < 32) kd[tid] = dnext;
     __syncthreads();
     const int kv0 = 32 * tile_of(i);
@@ -402,10 +449,14 @@ void attn_bwd_dq_f32(Args a) {
     if (__builtin_amdgcn_ballot_w64(okm != 0) == 0) continue;
     f32x16_t sacc = zero16(), pacc = zero16();
 #pragma unroll
-    for (int k = 0; k < NS; ++k)
-      if (2 * k < D) {
-        sacc = mfma(Ks[l32 * P + 2 * k + hh], qf[k], sacc);  // S^T = K Q^T
-        pacc = mfma(Vs[l32 * P + 2 * k + hh], gf[k], pacc);  // dP^T = V dO^T
+    for (int q4 = 0; q4 < NS / 4; ++q4)
+      if (8 * q4 < D) {
+        const f32x4_t ka = rs4<DP>(Ks, l32, hh, q4), va = rs4<DP>(Vs, l32, hh, q4);
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          sacc = mfma(ka[x], qf[4 * q4 + x], sacc);  // S^T = K Q^T
+          pacc = mfma(va[x], gf[4 * q4 + x], pacc);  // dP^T = V dO^T
+        }
       }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -417,8 +468,11 @@ void attn_bwd_dq_f32(Args a) {
     for (int db = 0; db < NDB; ++db)
       if (32 * db < D) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          dqacc[db] = mfma(Ks[crow(hh, r) * P + 32 * db + l32], sacc[r], dqacc[db]);
+        for (int g = 0; g < 4; ++g) {
+          const f32x4_t ka = tr4(Kt, db, l32, hh, g);
+#pragma unroll
+          for (int x = 0; x < 4; ++x) dqacc[db] = mfma(ka[x], sacc[4 * g + x], dqacc[db]);
+        }
       }
   }
   if (!qv) return;
@@ -439,8 +493,10 @@ template <int DP>
 __global__ __launch_bounds__(64 * kWaves)
 __attribute__((amdgpu_waves_per_eu(DP >= 64 ? 1 : 2, DP >= 64 ? 1 : 2)))
 void attn_bwd_dkdv_f32(Args a) {
-  constexpr int P = DP + 1, NS = DP / 2, NDB = DP / 32;
-  __shared__ float Qs[32 * P], Gs[32 * P];
+  constexpr int NS = DP / 2, NDB = DP / 32;
+  // Q and dO row-split (S, dP) and transposed (dK^T, dV^T).
+  __shared__ __align__(16) float Qs[Tile<DP>::kRsFloats], Gs[Tile<DP>::kRsFloats];
+  __shared__ __align__(16) float Qt[Tile<DP>::kTrFloats], Gt[Tile<DP>::kTrFloats];
   __shared__ int64_t qd[32];
   __shared__ float ls[32], dls[32];
   __shared__ Visit vis;
@@ -508,8 +564,10 @@ void attn_bwd_dkdv_f32(Args a) {
   fetch(i0);
   for (int t = i0; t < i1; ++t) {
     __syncthreads();
-    tq.store(Qs, vec);
-    tg.store(Gs, vec);
+    tq.store_rs(Qs, vec);
+    tq.store_tr(Qt, vec);
+    tg.store_rs(Gs, vec);
+    tg.store_tr(Gt, vec);
     if (tid < 32) qd[tid] = dnext;
     else if (tid < 64) ls[tid - 32] = lnext;
     else if (tid < 96) dls[tid - 64] = lnext;
@@ -525,10 +583,14 @@ void attn_bwd_dkdv_f32(Args a) {
     if (__builtin_amdgcn_ballot_w64(okm != 0) == 0) continue;
     f32x16_t sacc = zero16(), pacc = zero16();
 #pragma unroll
-    for (int k = 0; k < NS; ++k)
-      if (2 * k < D) {
-        sacc = mfma(Qs[l32 * P + 2 * k + hh], kf[k], sacc);  // S = Q K^T (lane <-> KV column)
-        pacc = mfma(Gs[l32 * P + 2 * k + hh], vf[k], pacc);  // dP = dO V^T
+    for (int q4 = 0; q4 < NS / 4; ++q4)
+      if (8 * q4 < D) {
+        const f32x4_t qa = rs4<DP>(Qs, l32, hh, q4), ga = rs4<DP>(Gs, l32, hh, q4);
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          sacc = mfma(qa[x], kf[4 * q4 + x], sacc);  // S = Q K^T (lane <-> KV column)
+          pacc = mfma(ga[x], vf[4 * q4 + x], pacc);  // dP = dO V^T
+        }
       }
     float pv[16];
 #pragma unroll
@@ -543,9 +605,13 @@ void attn_bwd_dkdv_f32(Args a) {
     for (int db = 0; db < NDB; ++db)
       if (32 * db < D) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          dvacc[db] = mfma(Gs[crow(hh, r) * P + 32 * db + l32], pv[r], dvacc[db]);
-          dkacc[db] = mfma(Qs[crow(hh, r) * P + 32 * db + l32], sacc[r], dkacc[db]);
+        for (int g = 0; g < 4; ++g) {
+          const f32x4_t ga = tr4(Gt, db, l32, hh, g), qa = tr4(Qt, db, l32, hh, g);
+#pragma unroll
+          for (int x = 0; x < 4; ++x) {
+            dvacc[db] = mfma(ga[x], pv[4 * g + x], dvacc[db]);
+            dkacc[db] = mfma(qa[x], sacc[4 * g + x], dkacc[db]);
+          }
         }
       }
   }

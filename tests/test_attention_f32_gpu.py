@@ -99,3 +99,27 @@ def test_f32_attention_empty_grad_paths(dev) -> None:
     (out * 0).sum().backward()
     for g in (qr.grad, kr.grad, vr.grad):
         assert g is not None and float(g.abs().max()) == 0.0
+
+
+def test_f32_backward_chunked_walks_repeat_bit_for_bit(dev) -> None:
+    """Small grids cut the dK/dV walk (heads x query sub-tiles) into chunks whose fp32
+    partials are summed in chunk order: two backward passes give identical bits, and the
+    workspace holds more than delta exactly when the grid is split."""
+    from packbalance_amd import _native as N
+
+    B, Hq, Hkv, S, D = 1, 12, 4, 2048, 64
+    packs = W.cfg2_steps(1)[0][:B]
+    doc = W.doc_ids_from_lengths(packs, S).to(dev)
+    q, k, v, do = _inputs(B, Hq, Hkv, S, D, dev, seed=21)
+    delta_bytes = B * Hq * S * 4
+    assert N.lib().pb_attn_bwd_f32_workspace_bytes(B, Hq, Hkv, S, D) > delta_bytes
+    # 8 packs x 8 KV heads x 64 KV tiles = 4096 tiles: no split, delta only
+    assert N.lib().pb_attn_bwd_f32_workspace_bytes(8, 32, 8, 8192, 128) == 8 * 32 * 8192 * 4
+    grads = []
+    for _ in range(2):
+        qr, kr, vr = (t.detach().requires_grad_(True) for t in (q, k, v))
+        doc_attention(qr, kr, vr, doc).backward(do)
+        torch.cuda.synchronize()
+        grads.append((qr.grad.clone(), kr.grad.clone(), vr.grad.clone()))
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)
