@@ -314,7 +314,10 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_loop(
 }
 
 // dw[c] = sum_p partial[p, c]: 64 columns x 16 partial-row groups per block,
-// each thread with four independent accumulators so the loads overlap.
+// each thread with four independent accumulators.  The loads of eight
+// iterations are issued before their sums (one memory round trip for the 512
+// partial rows of the usual plan instead of eight); the additions keep the
+// order of the one-iteration loop.
 template <typename TW>
 __global__ __launch_bounds__(1024) void rmsnorm_dw_reduce(const float *__restrict__ partial,
                                                           TW *__restrict__ dw, int nparts, int n) {
@@ -324,6 +327,20 @@ __global__ __launch_bounds__(1024) void rmsnorm_dw_reduce(const float *__restric
   float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
   if (col < n) {
     int p = grp;
+    for (; p + 64 * 7 + 48 < nparts; p += 64 * 8) {
+      float v[8][4];
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[k][q] = partial[(int64_t)(p + 64 * k + 16 * q) * n + col];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        s0 += v[k][0];
+        s1 += v[k][1];
+        s2 += v[k][2];
+        s3 += v[k][3];
+      }
+    }
     for (; p + 48 < nparts; p += 64) {
       s0 += partial[(int64_t)p * n + col];
       s1 += partial[(int64_t)(p + 16) * n + col];
