@@ -50,7 +50,7 @@ def _lognormal_pack(rng, seq_len, mu, sigma, lo, pad):
 def layouts() -> list[tuple[str, list[int], int]]:
     rng = np.random.default_rng(1234)
     L = []
-    L.append(("one_doc_256", [0] * 256, 2))  # SURVEY known answer
+    L.append(("one_doc_256", [0] * 256, 2))  # one document: the plain causal block mask
     L.append(("ref_test_64", [0] * 20 + [1] * 44, 2))  # tests/test_attention.py:211
     L.append(("pad_tail_300", [0] * 100 + [1] * 150 + [-1] * 50, 2))
     L.append(("lognormal_2048", _lognormal_pack(rng, 2048, np.log(200), 1.1, 8, 3), 12))

@@ -182,8 +182,8 @@ def test_fused_ce_grad_output_scaling(dev) -> None:
 
 
 def test_fused_ce_fp32_inputs_under_bf16_autocast(dev) -> None:
-    """The model's cfg2 flow: fp32 hidden states and the fp32 tied weight
-    under bf16 autocast.  The reference's product is then bf16 (autocast), so the kernel
+    """The model's cfg2 flow (packbalance/model/llama.py:225): fp32 hidden states and the
+    fp32 tied weight under bf16 autocast.  The reference's product is then bf16 (autocast), so the kernel
     path runs with bf16 operands and bf16 logits, against that oracle."""
     x, w, t = _case((2048,), 32000, 768, torch.float32, torch.float32, dev, seed=11, wstd=0.05,
                     ignore_every=7)
