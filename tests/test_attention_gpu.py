@@ -311,3 +311,95 @@ def test_attention_running_max_moves(profile, D, dev) -> None:
     # the absolute tolerance is scaled by the mean |K| entry (~3).
     torch.testing.assert_close(dq.detach().float().cpu(), ref["dq"].float(), atol=3 * TOL,
                                rtol=TOL, msg=lambda m: f"{what} dq: {m}")
+
+
+def _bwd_abi(q, k, v, out, do, lse, doc, outs=None):
+    """pb_attn_bwd through the C ABI on given forward results; dq / dk / dv as
+    [B, S, H, D] memory seen as [B, H, S, D] (the model's layout)."""
+    from packbalance_amd import _native as N
+    from packbalance_amd.model import attention as A
+
+    B, Hq, S, D = q.shape
+    Hkv = k.shape[1]
+    plans = A._plans(doc, Hq, Hkv, D, None)
+    if outs is None:
+        outs = (torch.empty(B, S, Hq, D, device=q.device, dtype=q.dtype).transpose(1, 2),
+                torch.empty(B, S, Hkv, D, device=q.device, dtype=q.dtype).transpose(1, 2),
+                torch.empty(B, S, Hkv, D, device=q.device, dtype=q.dtype).transpose(1, 2),
+                torch.empty(max(1, plans["workspace"]), dtype=torch.uint8, device=q.device))
+    dq, dk, dv, ws = outs
+    pq, pk = plans[A.BWD_Q], plans[A.BWD_KV]
+    N.call("pb_attn_bwd", N.BHSD.of(q), N.BHSD.of(k), N.BHSD.of(v), N.BHSD.of(out),
+           N.BHSD.of(do), N.BHSD.of(dq), N.BHSD.of(dk), N.BHSD.of(dv), lse.data_ptr(),
+           ws.data_ptr(), doc.data_ptr(), doc.stride(0), pq.counts.data_ptr(),
+           pq.lists.data_ptr(), pk.counts.data_ptr(), pk.lists.data_ptr(), B, Hq, Hkv, S, D,
+           1.0 / math.sqrt(D), N.PB_BF16, N.stream_ptr(q))
+    return outs
+
+
+def _fwd_abi(q, k, v, doc):
+    from packbalance_amd import _native as N
+    from packbalance_amd.model import attention as A
+
+    B, Hq, S, D = q.shape
+    Hkv = k.shape[1]
+    plans = A._plans(doc, Hq, Hkv, D, None)
+    out = torch.empty(B, S, Hq, D, device=q.device, dtype=q.dtype).transpose(1, 2)
+    lse = torch.empty(B, Hq, S, device=q.device, dtype=torch.float32)
+    fws = torch.empty(max(1, plans["fwd_workspace"]), dtype=torch.uint8, device=q.device)
+    p = plans[A.FWD]
+    N.call("pb_attn_fwd", N.BHSD.of(q), N.BHSD.of(k), N.BHSD.of(v), N.BHSD.of(out),
+           lse.data_ptr(), fws.data_ptr(), doc.data_ptr(), doc.stride(0), p.counts.data_ptr(),
+           p.lists.data_ptr(), B, Hq, Hkv, S, D, 1.0 / math.sqrt(D), N.PB_BF16,
+           N.stream_ptr(q))
+    return out, lse
+
+
+def test_kept_ds_backward_packs_independent(dev) -> None:
+    """The kept-dS backward (dK/dV storing dS, then dQ from it) is independent
+    of the batch around a pack: the gradients of a 4-pack call equal, bit for
+    bit, those of each pack alone, on the same forward results (per-pack
+    offsets of the plans, the dS blocks, lse and delta)."""
+    B, Hq, Hkv, S, D = 4, 32, 8, 8192, 128
+    doc = W.doc_ids_from_lengths(W.cfg3_packs()[:B], S).to(dev)
+    q, k, v, do = _inputs(B, Hq, Hkv, S, D, dev, seed=21)
+    out, lse = _fwd_abi(q, k, v, doc)
+    dq, dk, dv, _ = _bwd_abi(q, k, v, out, do, lse, doc)
+    for b in range(B):
+        sl = slice(b, b + 1)
+        dq1, dk1, dv1, _ = _bwd_abi(q[sl], k[sl], v[sl], out[sl], do[sl], lse[sl],
+                                    doc[sl].contiguous())
+        for name, got, want in (("dq", dq[sl], dq1), ("dk", dk[sl], dk1), ("dv", dv[sl], dv1)):
+            assert torch.equal(got, want), f"pack {b} {name} differs from the single-pack call"
+    assert torch.isfinite(dq.float()).all() and torch.isfinite(dk.float()).all()
+
+
+def test_kept_ds_backward_graph_replays(dev) -> None:
+    """The kept-dS backward captured into a HIP graph: every replay, with eager
+    work and synchronisations between them and the outputs poisoned before
+    each, gives the eager call's gradients bit for bit."""
+    B, Hq, Hkv, S, D = 2, 32, 8, 8192, 128
+    doc = W.doc_ids_from_lengths(W.cfg3_packs()[1 : 1 + B], S).to(dev)
+    q, k, v, do = _inputs(B, Hq, Hkv, S, D, dev, seed=22)
+    out, lse = _fwd_abi(q, k, v, doc)
+    want = [t.clone() for t in _bwd_abi(q, k, v, out, do, lse, doc)[:3]]
+    torch.cuda.synchronize()
+    outs = _bwd_abi(q, k, v, out, do, lse, doc)  # static outputs and workspace
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        _bwd_abi(q, k, v, out, do, lse, doc, outs)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _bwd_abi(q, k, v, out, do, lse, doc, outs)
+    for rep in range(3):
+        for t in outs[:3]:
+            t.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, got, w in zip(("dq", "dk", "dv"), outs[:3], want):
+            assert torch.equal(got, w), f"replay {rep}: {name} differs from the eager call"
+        _ = (q.float() * 2).sum().item()  # eager work between replays
